@@ -1,0 +1,283 @@
+"""Benchmark: ModernBERT-base encode tokens/s at B=32, T=512 on one MI355X.
+
+One step = one full encoder forward (embeddings + 22 layers + final norm)
+over a batch of 32 sequences of 512 tokens (lengths uniform in [64, 512],
+right-padded), through HipBackend, the laya-js `Backend`
+contract on libhipbackend.so, driven by the unchanged encoder code.  Inputs
+(token ids, masks) are resident on the GPU before the timed region.  Weights
+are random-init fp16 ~N(0, 0.02) with LayerNorm gamma = 1; ids uniform in
+[0, 50368).
+
+Prints ONE JSON line on stdout.  Also reported:
+- roofline of the dominant kernel family (the linear-layer MFMA GEMMs:
+  4 launches per layer), from HIP events around each launch in a profiled
+  pass after the timed region;
+- cpu_baseline: the CPU oracle (a C restatement of the reference's CPU
+  backend, OpenMP over the host cores) on a bounded sample of the same
+  workload.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+  python bench.py --mode gemm    # isolated config-1/2 GEMM sweep (stderr table + JSON lines)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "laya-js_amd"))
+
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (spec)
+PEAK_HBM_GBS = 8000.0
+
+BASE = {"vocab_size": 50368, "hidden_size": 768, "intermediate_size": 1152, "num_hidden_layers": 22,
+        "num_attention_heads": 12, "local_attention": 128}
+METRIC = "ModernBERT-base encode tokens/s at B=32,T=512; linear-layer MFMA util %"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_weights(cfg: dict, seed: int = 0) -> dict:
+    """Random-init fp16 encoder weights (names without the 'encoder.' prefix)."""
+    rng = np.random.default_rng(seed)
+    H, I, V, Lr = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
+
+    def n(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * 0.02).astype(np.float16)
+    W = {"embeddings.tok_embeddings.weight": n(V, H), "embeddings.norm.weight": np.ones(H, np.float16),
+         "final_norm.weight": np.ones(H, np.float16)}
+    for i in range(Lr):
+        p = f"layers.{i}."
+        if i:
+            W[p + "attn_norm.weight"] = np.ones(H, np.float16)
+        W[p + "attn.Wqkv.weight"] = n(3 * H, H)
+        W[p + "attn.Wo.weight"] = n(H, H)
+        W[p + "mlp_norm.weight"] = np.ones(H, np.float16)
+        W[p + "mlp.Wi.weight"] = n(2 * I, H)
+        W[p + "mlp.Wo.weight"] = n(H, I)
+    return W
+
+
+def linear_flops_per_forward(cfg: dict, M: int) -> float:
+    H, I, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
+    per_layer = 2 * M * (3 * H * H + H * H + 2 * I * H + H * I)
+    return float(per_layer * L)
+
+
+def run_encode(args) -> dict:
+    from laya_hip.backend import HipBackend
+    from laya_hip.host import HostTensor
+    from laya_hip.modernbert import loadModernBert, parseModernBertConfig
+
+    B, T = 32, 512
+    cfg = parseModernBertConfig(BASE)
+    W = make_weights(BASE)
+    rng = np.random.default_rng(1)
+    lens = rng.integers(64, T + 1, B)
+    ids = rng.integers(0, BASE["vocab_size"], (B, T)).astype(np.int32)
+    valid = (np.arange(T)[None, :] < lens[:, None]).astype(np.uint8)
+
+    be = HipBackend(0)
+    info = be.device_info()
+    log(f"device: {info}")
+    t0 = time.time()
+    enc = loadModernBert(be, cfg, lambda nm: HostTensor("f16", W[nm[8:]].shape, W[nm[8:]])
+                         if nm.startswith("encoder.") and nm[8:] in W else None, dtype="f16")
+    inp = enc.uploadInputs(ids, valid, B, T)
+    be.flush()
+    log(f"weights + inputs resident in {time.time() - t0:.1f}s")
+
+    def step():
+        y = enc.encode(inp)
+        return y
+
+    for _ in range(args.warmup):
+        be.dispose(step())
+    be.flush()
+    ev0, ev1 = be.event(), be.event()
+    be.flush()
+    wall0 = time.perf_counter()
+    be.record(ev0)
+    for _ in range(args.steps):
+        be.dispose(step())
+    be.record(ev1)
+    be.flush()
+    wall = time.perf_counter() - wall0
+    gpu_ms = be.elapsed_ms(ev0, ev1)
+    ms_per_step = gpu_ms / args.steps
+    tokens = B * T
+    valid_tokens = int(valid.sum())
+    log(f"timed {args.steps} steps: {gpu_ms:.2f} ms on the stream ({wall * 1e3:.2f} ms wall) "
+        f"-> {ms_per_step:.3f} ms/step")
+
+    # profiled pass (after the timed region): per-launch GPU time by op key
+    be.startProfiling()
+    for _ in range(args.profile_steps):
+        be.dispose(step())
+    prof = be.stopProfiling()
+    lin_ms = sum(t for k, (n, t) in prof.items() if k.startswith(("linear[", "quantizedLinear[")))
+    lin_launches = sum(n for k, (n, t) in prof.items() if k.startswith(("linear[", "quantizedLinear[")))
+    lin_ms /= args.profile_steps
+    lin_launches //= args.profile_steps
+    prof_total = sum(t for (n, t) in prof.values()) / args.profile_steps
+    lin_flops = linear_flops_per_forward(BASE, tokens)
+    achieved = lin_flops / (lin_ms * 1e-3) / 1e12
+    log("profiled pass (per forward):")
+    for k, (n, t) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        log(f"  {k:58s} launches {n // args.profile_steps:4d}  {t / args.profile_steps:8.3f} ms")
+    log(f"  sum of kernel times {prof_total:.3f} ms vs timed step {ms_per_step:.3f} ms")
+
+    out = be.read(step())
+    finite = bool(np.isfinite(out.data.astype(np.float32)).all())
+    enc.disposeInputs(inp)
+    enc.dispose()
+    be.destroy()
+
+    res = {
+        "metric": METRIC,
+        "value": tokens / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (random-init fp16 weights ~N(0,0.02), ids U[0,50368), lengths U[64,512] right-padded)",
+        "config": {
+            "workload": "BASELINE config 3: ModernBERT-base-shape encoder forward, B=32, T=512, 22 layers, "
+                        "hidden 768, 12 heads, GeGLU 1152, local window 128 / global every 3rd layer",
+            "global_batch": B, "seq_len": T, "parallelism": "single GPU",
+            "padded_tokens_per_step": tokens, "valid_tokens_per_step": valid_tokens,
+            "valid_tokens_per_s": valid_tokens / (ms_per_step * 1e-3),
+            "linear_tflop_per_step": lin_flops / 1e12,
+            "linear_ms_per_step": lin_ms, "linear_launches_per_step": lin_launches,
+            "linear_mfma_util_pct": 100.0 * achieved / PEAK_F16_TFLOPS,
+            "output_finite": finite, "device": info.get("name"),
+        },
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_F16_TFLOPS, "traffic": None,
+                     "kernel": "gemm_mfma (the 4 linear layers of every encoder layer; algorithmic 2*M*N*K "
+                               f"= {lin_flops / 1e12:.3f} TFLOP per forward over {lin_launches} launches)"},
+    }
+    return res
+
+
+def cpu_baseline(sample_b: int = 8) -> dict:
+    """The CPU oracle (C, OpenMP, f64 accumulation) on `sample_b` of the 32
+    sequences at T=512, all 22 layers; reported as tokens/s of that sample."""
+    from oracle import cpu_ref as cr
+    sys.path.insert(0, ROOT)
+    B, T = sample_b, 512
+    W = {k: v.astype(np.float32) for k, v in make_weights(BASE).items()}
+    rng = np.random.default_rng(1)
+    lens = rng.integers(64, T + 1, 32)[:B]
+    ids = rng.integers(0, BASE["vocab_size"], (32, T)).astype(np.int32)[:B]
+    valid = (np.arange(T)[None, :] < lens[:, None]).astype(np.uint8)
+    cfg = cr.EncoderConfig.from_json(BASE)
+    t0 = time.perf_counter()
+    y = cr.encoder_forward(cfg, W, ids, valid)
+    dt = time.perf_counter() - t0
+    assert np.isfinite(y).all()
+    cpu = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": B * T / dt, "unit": "tokens/s", "cores": cr.num_threads(), "kind": "port",
+            "sample": f"{B} of the 32 sequences (T=512, padded, all 22 layers) in {dt:.1f}s on {cpu}; "
+                      "C restatement of the reference CPU backend (f32 storage, f64 accumulation)"}
+
+
+def run_gemm_sweep(args) -> None:
+    """BASELINE configs 1 and 2: isolated linears at M in {128..16384}."""
+    from laya_hip import compose as C
+    from laya_hip.backend import HipBackend
+    from laya_hip.host import HostQuantized, HostTensor, pack_quantized
+    from laya_hip.quant import quantize_matrix
+
+    be = HipBackend(0)
+    rng = np.random.default_rng(0)
+    shapes = [("Wqkv", 2304, 768, False), ("Wo", 768, 768, False), ("Wi+GeGLU", 2304, 768, True),
+              ("WoMlp", 768, 1152, False)]
+    log(f"{'shape':10s} {'M':>6s} {'kind':>5s} {'us':>9s} {'TFLOP/s':>8s} {'%peak':>6s}")
+    for name, N, K, geglu in shapes:
+        w = (rng.standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float16)
+        Wt = be.fromHost(HostTensor("f16", (N, K), w))
+        quants = {}
+        for bits in (8, 4):
+            q, s, z = quantize_matrix(w.astype(np.float32), N, K, bits, 64, refine=bits == 4)
+            h = HostQuantized((N, K), bits, 64, "symmetric" if bits == 8 else "affine", pack_quantized(q, bits),
+                              HostTensor("f16", s.shape, s), HostTensor("f16", z.shape, z) if z is not None else None)
+            quants[bits] = C.upload_quantized(be, h, "f16")
+        for M in (128, 512, 2048, 8192, 16384):
+            X = be.fromHost(HostTensor("f16", (M, K), rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)))
+            kinds = [("f16", lambda: be.linear(X, Wt))]
+            if M in (512, 8192):
+                kinds += [(f"q{b}", (lambda b=b: C.quantized_linear(be, X, quants[b]))) for b in (8, 4)]
+            for kind, fn in kinds:
+                def launch():
+                    y = fn()
+                    return be.geglu(y) if geglu else be._ready(y)
+                for _ in range(3):
+                    be.dispose(launch())
+                reps = max(5, int(2e11 / (2 * M * N * K)))
+                a, b = be.event(), be.event()
+                be.flush()
+                be.record(a)
+                for _ in range(reps):
+                    be.dispose(launch())
+                be.record(b)
+                ms = be.elapsed_ms(a, b) / reps
+                tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+                log(f"{name:10s} {M:6d} {kind:>5s} {ms * 1e3:9.1f} {tf:8.1f} {100 * tf / PEAK_F16_TFLOPS:6.1f}")
+                print(json.dumps({"shape": name, "M": M, "N": N, "K": K, "kind": kind, "us": ms * 1e3,
+                                  "tflops": tf, "mfma_util_pct": 100 * tf / PEAK_F16_TFLOPS}), flush=True)
+            be.dispose(X)
+    be.destroy()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--profile-steps", type=int, default=2)
+    ap.add_argument("--mode", choices=["encode", "gemm"], default="encode")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-sample", type=int, default=8, help="sequences in the CPU-baseline sample")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the encoder is "
+              "data-parallel over sequences and would shard by batch rows with no collectives -- see DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.mode == "gemm":
+        run_gemm_sweep(args)
+        return
+    res = run_encode(args)
+    if not args.no_cpu:
+        log("timing the CPU baseline ...")
+        res["cpu_baseline"] = cpu_baseline(args.cpu_sample)
+        log(f"cpu baseline: {res['cpu_baseline']}")
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

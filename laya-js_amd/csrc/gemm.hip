@@ -1,0 +1,595 @@
+// Linear layers: y = x . w^T with f32 accumulation and fused epilogues, for
+// 16-bit weights and for laya's quantized weight format (q8 / q4 with
+// per-group scales and zeros).
+//
+// The hot path is gemm_mfma: fp16 / bf16 operands on gfx950's
+// v_mfma_f32_16x16x32_{f16,bf16}, both operands K-contiguous ("NT"), A and B
+// tiles double-buffered in LDS (64-wide K stages, 16-byte chunks XOR-swizzled
+// by row so the fragment reads of 16 consecutive rows spread over the banks),
+// and an epilogue that adds bias, rounds once to the storage type, applies
+// GeGLU on (value, gate) column pairs held by the same lane, stages the tile in
+// LDS and writes it with 16-byte coalesced stores, adding the residual there.
+// For quantized weights the B loader fetches the packed codes (8 or 4 bytes
+// per 8 weights) and the group's scale / zero, dequantizes them in registers
+// to fl16(q*s + z) -- one correctly rounded f16 fma, the value host
+// dequantization would upload -- and stages f16 into LDS for the same MFMA.
+// Blocks walk the tile grid in an XCD-aware order: the hardware deals block b
+// to XCD b % 8, so block b is given the tile that keeps each XCD on a
+// contiguous run of row panels (their A rows and the whole W stay in that
+// XCD's L2).
+//
+// gemm_simt is the f32 path (and the fallback for shapes the MFMA kernel's
+// 16-byte loads cannot take: K or row strides not a multiple of 8).
+#include <stdexcept>
+
+#include "common.h"
+
+namespace hb {
+
+// ------------------------------------------------------------------ helpers
+
+template <bool BF16>
+__device__ __forceinline__ float4v mfma16(const uint4v& a, const uint4v& b, float4v c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                  0, 0);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float to_f(uint32_t h) {
+  return BF16 ? bf16_to_f32((uint16_t)h) : f16_bits_to_f32((uint16_t)h);
+}
+template <bool BF16>
+__device__ __forceinline__ uint16_t from_f(float v) {
+  return BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+}
+
+// LDS element offset of 16-byte chunk c of row r in a [rows][64] u16 tile.
+__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+
+// Tile index for block `bid` of `nb`: contiguous runs of tiles per XCD.
+__device__ __forceinline__ int xcd_tile(int bid, int nb) {
+  int xcd = bid & 7, idx = bid >> 3;
+  int q = nb >> 3, rem = nb & 7;
+  return xcd * q + (xcd < rem ? xcd : rem) + idx;
+}
+
+// Quantized code e (0..7) of a chunk: q8 codes are bytes of (w0, w1), q4
+// codes nibbles of w0 (even column in the low nibble).
+template <int QB, bool AFF>
+__device__ __forceinline__ int qcode(uint32_t w0, uint32_t w1, int e) {
+  if constexpr (QB == 8) {
+    uint32_t w = e < 4 ? w0 : w1;
+    int sh = 8 * (e & 3);
+    return AFF ? (int)((w >> sh) & 0xff) : (int)(int8_t)((w >> sh) & 0xff);
+  } else {
+    int v = (int)((w0 >> (4 * e)) & 0xf);
+    return AFF ? v : ((v ^ 8) - 8);
+  }
+}
+
+// 8 dequantized weights as 16-bit values.  f16 with f16 scales: one f16 fma
+// (q is exact in f16), so the weight is fl16(q*s + z) rounded once.  Other
+// combinations compute in f32 and round once to the storage type.
+template <int QB, bool AFF, bool SF32, bool BF16>
+__device__ __forceinline__ uint4v dequant8(uint32_t w0, uint32_t w1, uint32_t sbits, uint32_t zbits, float sf,
+                                           float zf) {
+  uint32_t out[4];
+  if constexpr (!SF32 && !BF16) {
+    f16 s, z;
+    uint16_t sb = (uint16_t)sbits, zb = (uint16_t)zbits;
+    __builtin_memcpy(&s, &sb, 2);
+    __builtin_memcpy(&z, &zb, 2);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      f16 q0 = (f16)(float)qcode<QB, AFF>(w0, w1, e), q1 = (f16)(float)qcode<QB, AFF>(w0, w1, e + 1);
+      f16 r0 = AFF ? __builtin_fmaf16(q0, s, z) : (f16)(q0 * s);
+      f16 r1 = AFF ? __builtin_fmaf16(q1, s, z) : (f16)(q1 * s);
+      uint16_t b0, b1;
+      __builtin_memcpy(&b0, &r0, 2);
+      __builtin_memcpy(&b1, &r1, 2);
+      out[e >> 1] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+    }
+  } else {
+    const float s = SF32 ? sf : f16_bits_to_f32((uint16_t)sbits);
+    const float z = SF32 ? zf : f16_bits_to_f32((uint16_t)zbits);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float q0 = (float)qcode<QB, AFF>(w0, w1, e), q1 = (float)qcode<QB, AFF>(w0, w1, e + 1);
+      float r0 = AFF ? fmaf(q0, s, z) : q0 * s;
+      float r1 = AFF ? fmaf(q1, s, z) : q1 * s;
+      out[e >> 1] = (uint32_t)from_f<BF16>(r0) | ((uint32_t)from_f<BF16>(r1) << 16);
+    }
+  }
+  return uint4v{out[0], out[1], out[2], out[3]};
+}
+
+struct QW {  // quantized weight operand
+  const uint8_t* q;
+  const void* scales;
+  const void* zeros;
+  int G;      // groups per row
+  int group;  // values per group
+};
+
+// ------------------------------------------------------------------ MFMA kernel
+
+template <int BM, int BN, int WM, int WN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restrict__ X, int64_t ldx,
+                                                         const uint16_t* __restrict__ W, QW qw,
+                                                         const uint16_t* __restrict__ bias,
+                                                         const uint16_t* __restrict__ R, int64_t ldr,
+                                                         uint16_t* __restrict__ Y, int64_t ldy, int M, int N, int K,
+                                                         int tiles_n) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int BK = 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int TM = WTM / 16, TN = WTN / 16;  // 16x16 blocks per wave
+  constexpr int A_LD = BM * 8 / NT, B_LD = BN * 8 / NT;
+  constexpr int BNO = GEGLU ? BN / 2 : BN;  // output columns per tile
+  static_assert(A_LD * NT == BM * 8 && B_LD * NT == BN * 8, "tile/threads mismatch");
+  static_assert(!GEGLU || (TN % 2 == 0), "GEGLU needs an even number of column blocks per wave");
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* As = smem;                // [2][BM*64]
+  uint16_t* Bs = smem + 2 * BM * BK;  // [2][BN*64]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int m0 = (tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BNO;  // first output column (pair index for GEGLU)
+
+  // B tile row r -> W row (GEGLU: first half value rows, second half gate rows)
+  auto w_row = [&](int r) -> int {
+    if constexpr (GEGLU) return r < BN / 2 ? n0 + r : N + n0 + (r - BN / 2);
+    else return n0 + r;
+  };
+  auto w_valid = [&](int r) -> bool {
+    if constexpr (GEGLU) return n0 + (r < BN / 2 ? r : r - BN / 2) < N;
+    else return n0 + r < N;
+  };
+
+  uint4v ra[A_LD], rb[B_LD];
+  uint32_t rs[QB ? B_LD : 1], rz[QB ? B_LD : 1];
+  float rsf[QB && SF32 ? B_LD : 1], rzf[QB && SF32 ? B_LD : 1];
+  auto load_regs = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      int k = k0 + c * 8;
+      if (m0 + r < M && k < K) ra[i] = *(const uint4v*)(X + (int64_t)(m0 + r) * ldx + k);
+      else ra[i] = uint4v{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      int k = k0 + c * 8;
+      bool ok = w_valid(r) && k < K;
+      if constexpr (QB == 0) {
+        rb[i] = ok ? *(const uint4v*)(W + (int64_t)w_row(r) * K + k) : uint4v{0, 0, 0, 0};
+      } else {
+        rb[i] = uint4v{0, 0, 0, 0};
+        rs[i] = rz[i] = 0;
+        if constexpr (SF32) rsf[i] = rzf[i] = 0.f;
+        if (ok) {
+          int64_t row = w_row(r);
+          if constexpr (QB == 8) {
+            uint2v w = *(const uint2v*)(qw.q + row * K + k);
+            rb[i].x = w.x;
+            rb[i].y = w.y;
+          } else {
+            rb[i].x = *(const uint32_t*)(qw.q + row * (K / 2) + k / 2);
+          }
+          int64_t gi = row * qw.G + k / qw.group;
+          if constexpr (SF32) {
+            rsf[i] = ((const float*)qw.scales)[gi];
+            if constexpr (AFF) rzf[i] = ((const float*)qw.zeros)[gi];
+          } else {
+            rs[i] = ((const uint16_t*)qw.scales)[gi];
+            if constexpr (AFF) rz[i] = ((const uint16_t*)qw.zeros)[gi];
+          }
+        }
+      }
+    }
+  };
+  auto store_lds = [&](int buf) {
+    uint16_t* a = As + buf * BM * BK;
+    uint16_t* b = Bs + buf * BN * BK;
+#pragma unroll
+    for (int i = 0; i < A_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      *(uint4v*)(a + swz(r, c)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      if constexpr (QB == 0) {
+        *(uint4v*)(b + swz(r, c)) = rb[i];
+      } else {
+        float sf = 0.f, zf = 0.f;
+        if constexpr (SF32) {
+          sf = rsf[i];
+          zf = rzf[i];
+        }
+        *(uint4v*)(b + swz(r, c)) = dequant8<QB, AFF, SF32, BF16>(rb[i].x, rb[i].y, rs[i], rz[i], sf, zf);
+      }
+    }
+  };
+
+  // column block tn of this wave -> tile column (B tile row)
+  auto bcol = [&](int tn) -> int {
+    if constexpr (GEGLU) {
+      constexpr int H = TN / 2;
+      return tn < H ? wn * (WTN / 2) + tn * 16 : BN / 2 + wn * (WTN / 2) + (tn - H) * 16;
+    } else {
+      return wn * WTN + tn * 16;
+    }
+  };
+
+  float4v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = (K + BK - 1) / BK;
+  load_regs(0);
+  store_lds(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; kt++) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) load_regs((kt + 1) * BK);
+    const uint16_t* a = As + buf * BM * BK;
+    const uint16_t* b = Bs + buf * BN * BK;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      const int c = s * 4 + (lane >> 4);
+      uint4v af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) af[i] = *(const uint4v*)(a + swz(wm * WTM + i * 16 + (lane & 15), c));
+#pragma unroll
+      for (int j = 0; j < TN; j++) bf[j] = *(const uint4v*)(b + swz(bcol(j) + (lane & 15), c));
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = mfma16<BF16>(af[i], bf[j], acc[i][j]);
+    }
+    if (kt + 1 < KT) store_lds(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: bias, one rounding, GeGLU, stage in LDS as [BM][BNO]
+  uint16_t* Cs = smem;
+  constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
+  constexpr int WTNO = GEGLU ? WTN / 2 : WTN;
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+#pragma unroll
+    for (int j = 0; j < OUT_TN; j++) {
+      const int ocol = wn * WTNO + j * 16 + (lane & 15);  // tile output column
+      const int gcol = n0 + ocol;
+      float bv = 0.f, bg = 0.f;
+      if (bias != nullptr && gcol < N) {
+        bv = to_f<BF16>(bias[gcol]);
+        if constexpr (GEGLU) bg = to_f<BF16>(bias[N + gcol]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int orow = wm * WTM + i * 16 + (lane >> 4) * 4 + r;
+        float v = to_f<BF16>(from_f<BF16>(acc[i][j][r] + bv));
+        if constexpr (GEGLU) {
+          float g = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][r] + bg));
+          v = gelu_erf(v) * g;
+        }
+        Cs[orow * BNO + ocol] = from_f<BF16>(v);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- coalesced write-out (16-byte chunks), residual added here
+  constexpr int CPR = BNO / 8;  // chunks per row
+  for (int q = tid; q < BM * CPR; q += NT) {
+    const int r = q / CPR, c = q % CPR;
+    const int gm = m0 + r, gn = n0 + c * 8;
+    if (gm >= M || gn >= N) continue;
+    uint4v v = *(const uint4v*)(Cs + r * BNO + c * 8);
+    if (gn + 8 <= N) {
+      if (R != nullptr) {
+        uint4v rv = *(const uint4v*)(R + (int64_t)gm * ldr + gn);
+        uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t rr[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          uint16_t lo = from_f<BF16>(to_f<BF16>(vv[e] & 0xffff) + to_f<BF16>(rr[e] & 0xffff));
+          uint16_t hi = from_f<BF16>(to_f<BF16>(vv[e] >> 16) + to_f<BF16>(rr[e] >> 16));
+          vv[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        v = uint4v{vv[0], vv[1], vv[2], vv[3]};
+      }
+      *(uint4v*)(Y + (int64_t)gm * ldy + gn) = v;
+    } else {
+      uint16_t vs[8];
+      __builtin_memcpy(vs, &v, 16);
+      for (int e = 0; e < 8 && gn + e < N; e++) {
+        uint16_t o = vs[e];
+        if (R != nullptr) o = from_f<BF16>(to_f<BF16>(o) + to_f<BF16>(R[(int64_t)gm * ldr + gn + e]));
+        Y[(int64_t)gm * ldy + gn + e] = o;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ SIMT kernel (f32 path, fallback)
+
+struct QWs {  // quantized weight for the SIMT kernel (bits = 0: plain)
+  const uint8_t* q;
+  const void* scales;
+  const void* zeros;
+  int sdt;  // dtype of scales / zeros
+  int G, group, bits, aff;
+};
+
+__device__ __forceinline__ float simt_w(int dt, const void* W, const QWs& qw, int64_t n, int k, int K) {
+  if (qw.bits == 0) return load_f(W, n * K + k, dt);
+  int code;
+  if (qw.bits == 8) {
+    uint8_t u = qw.q[n * K + k];
+    code = qw.aff ? (int)u : (int)(int8_t)u;
+  } else {
+    uint8_t u = qw.q[n * (K / 2) + k / 2];
+    int v = (k & 1) ? (u >> 4) : (u & 15);
+    code = qw.aff ? v : ((v ^ 8) - 8);
+  }
+  int64_t gi = n * qw.G + k / qw.group;
+  float s = load_f(qw.scales, gi, qw.sdt);
+  // compose.ts:379-398: w = f32(f32(q*s) + z), rounded once to the compute dtype
+  float w = (float)code * s;
+  if (qw.aff) w = w + load_f(qw.zeros, gi, qw.sdt);
+  return round_to(w, dt);
+}
+
+// 64x64 output tile, 256 threads x (4x4) outputs, K staged 16 at a time.
+__global__ __launch_bounds__(256) void gemm_simt(int dt, const void* __restrict__ X, int64_t ldx,
+                                                 const void* __restrict__ W, QWs qw, const void* __restrict__ bias,
+                                                 const void* __restrict__ R, int64_t ldr, void* __restrict__ Y,
+                                                 int64_t ldy, int M, int N, int K, int geglu) {
+  __shared__ float As[16][64 + 1];
+  __shared__ float Bs[2][16][64 + 1];
+  const int tid = threadIdx.x;
+  const int tx = tid % 16, ty = tid / 16;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  float acc[2][4][4] = {};
+  const int nb = geglu ? 2 : 1;
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int q = tid; q < 16 * 64; q += 256) {
+      int r = q / 16, kk = q % 16;
+      int gm = m0 + r, gk = k0 + kk;
+      As[kk][r] = (gm < M && gk < K) ? load_f(X, (int64_t)gm * ldx + gk, dt) : 0.f;
+      for (int h = 0; h < nb; h++) {
+        int gn = n0 + r;
+        Bs[h][kk][r] = (gn < N && gk < K) ? simt_w(dt, W, qw, (int64_t)gn + (int64_t)h * N, gk, K) : 0.f;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; kk++) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) a[i] = As[kk][ty * 4 + i];
+      for (int h = 0; h < nb; h++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) b[j] = Bs[h][kk][tx * 4 + j];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) acc[h][i][j] = fmaf(a[i], b[j], acc[h][i][j]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int gm = m0 + ty * 4 + i;
+    if (gm >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      int gn = n0 + tx * 4 + j;
+      if (gn >= N) continue;
+      float v = acc[0][i][j] + (bias ? load_f(bias, gn, dt) : 0.f);
+      v = round_to(v, dt);
+      if (geglu) {
+        float g = round_to(acc[1][i][j] + (bias ? load_f(bias, N + gn, dt) : 0.f), dt);
+        v = gelu_erf(v) * g;
+      }
+      if (R) v = round_to(v, dt) + load_f(R, (int64_t)gm * ldr + gn, dt);
+      store_f(Y, (int64_t)gm * ldy + gn, dt, v);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+
+template <int BM, int BN, int WM, int WN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
+static void launch_mfma(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
+                        const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
+                        int K) {
+  constexpr int BNO = GEGLU ? BN / 2 : BN;
+  int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BNO - 1) / BNO;
+  size_t stage = (size_t)2 * (BM + BN) * 64 * sizeof(uint16_t);
+  size_t ctile = (size_t)BM * BNO * sizeof(uint16_t);
+  size_t lds = stage > ctile ? stage : ctile;
+  auto kern = gemm_mfma<BM, BN, WM, WN, BF16, GEGLU, QB, AFF, SF32>;
+  static bool attr = false;
+  if (!attr) {
+    HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = true;
+  }
+  kern<<<tiles_m * tiles_n, WM * WN * 64, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n);
+}
+
+template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
+static void mfma_dispatch(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
+                          const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
+                          int K) {
+  // 256x128 tiles (4 waves of 128x64) for large M, 128x128 otherwise
+  if ((int64_t)M >= 4096)
+    launch_mfma<256, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  else
+    launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+}
+
+template <int QB, bool AFF, bool SF32>
+static void mfma_dtype(int dt, bool geglu, hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
+                       const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
+                       int K) {
+  if (dt == HB_F16) {
+    if (geglu) mfma_dispatch<false, true, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    else mfma_dispatch<false, false, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  } else {
+    if (geglu) mfma_dispatch<true, true, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    else mfma_dispatch<true, false, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  }
+}
+
+static void check_linear_args(int dt, int64_t ldx, int64_t ldy, int64_t M, int64_t N, int64_t K, unsigned flags,
+                              uintptr_t bias, uintptr_t resid, int64_t ldr) {
+  HB_REQUIRE(dt == HB_F32 || dt == HB_F16 || dt == HB_BF16, "dtype must be f32, f16 or bf16");
+  HB_REQUIRE(M >= 0 && N >= 0 && K >= 0, "negative size");
+  HB_REQUIRE(M < (1ll << 31) && N < (1ll << 30) && K < (1ll << 30), "size too large");
+  HB_REQUIRE(ldx >= K && ldy >= N, "leading dimension smaller than the row");
+  HB_REQUIRE(!(flags & HB_EPI_BIAS) || bias, "bias flag without bias");
+  HB_REQUIRE(!(flags & HB_EPI_RESID) || (resid && ldr >= N), "resid flag without resid");
+}
+
+}  // namespace hb
+
+using namespace hb;
+
+extern "C" int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintptr_t w, uintptr_t bias,
+                         uintptr_t resid, int64_t ldr, uintptr_t y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                         unsigned flags) {
+  HB_API_BEGIN
+  try {
+    check_linear_args(dt, ldx, ldy, M, N, K, flags, bias, resid, ldr);
+  } catch (const std::exception& e) {
+    throw std::runtime_error(std::string("hb_linear: ") + e.what());
+  }
+  bool geglu = flags & HB_EPI_GEGLU;
+  const void* b = (flags & HB_EPI_BIAS) ? (const void*)bias : nullptr;
+  const void* r = (flags & HB_EPI_RESID) ? (const void*)resid : nullptr;
+  if (M == 0 || N == 0) return 0;
+  hipStream_t st = stream_of(ctx);
+  bool mfma = (dt == HB_F16 || dt == HB_BF16) && K > 0 && K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 &&
+              (!r || ldr % 8 == 0) && x % 16 == 0 && w % 16 == 0 && y % 16 == 0 && (!r || resid % 16 == 0);
+  if (mfma) {
+    QW qw{nullptr, nullptr, nullptr, 0, 1};
+    mfma_dtype<0, false, false>(dt, geglu, st, (const uint16_t*)x, ldx, (const uint16_t*)w, qw, (const uint16_t*)b,
+                                (const uint16_t*)r, ldr, (uint16_t*)y, ldy, (int)M, (int)N, (int)K);
+  } else {
+    QWs qw{nullptr, nullptr, nullptr, 0, 0, 1, 0, 0};
+    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+    gemm_simt<<<grid, 256, 0, st>>>(dt, (const void*)x, ldx, (const void*)w, qw, b, r, ldr, (void*)y, ldy, (int)M,
+                                    (int)N, (int)K, geglu ? 1 : 0);
+  }
+  check_launch("hb_linear");
+  HB_API_END
+}
+
+extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintptr_t qw, uintptr_t scales,
+                          uintptr_t zeros, uintptr_t bias, uintptr_t resid, int64_t ldr, uintptr_t y, int64_t ldy,
+                          int64_t M, int64_t N, int64_t K, int bits, int group, int mode, unsigned flags) {
+  HB_API_BEGIN
+  try {
+    check_linear_args(dt, ldx, ldy, M, N, K, flags, bias, resid, ldr);
+  } catch (const std::exception& e) {
+    throw std::runtime_error(std::string("hb_qlinear: ") + e.what());
+  }
+  HB_REQUIRE(bits == 8 || bits == 4, "hb_qlinear: bits must be 8 or 4");
+  HB_REQUIRE(mode == 0 || mode == 1, "hb_qlinear: mode must be 0 (symmetric) or 1 (affine)");
+  HB_REQUIRE(group > 0, "hb_qlinear: bad group size");
+  HB_REQUIRE((K * bits) % 32 == 0, "hb_qlinear: in * bits must be a multiple of 32");
+  HB_REQUIRE(qw && scales && (mode == 0 || zeros), "hb_qlinear: missing weight tensors");
+  bool geglu = flags & HB_EPI_GEGLU;
+  const void* b = (flags & HB_EPI_BIAS) ? (const void*)bias : nullptr;
+  const void* r = (flags & HB_EPI_RESID) ? (const void*)resid : nullptr;
+  if (M == 0 || N == 0) return 0;
+  hipStream_t st = stream_of(ctx);
+  int G = (int)((K + group - 1) / group);
+  // scales / zeros are f16 [N, G]: the laya checkpoint format
+  bool mfma = (dt == HB_F16 || dt == HB_BF16) && K > 0 && K % 8 == 0 && group % 8 == 0 && ldx % 8 == 0 &&
+              ldy % 8 == 0 && (!r || ldr % 8 == 0) && x % 16 == 0 && y % 16 == 0 && (!r || resid % 16 == 0) &&
+              qw % 8 == 0 && scales % 2 == 0 && zeros % 2 == 0;
+  if (mfma) {
+    QW q{(const uint8_t*)qw, (const void*)scales, (const void*)zeros, G, group};
+    const uint16_t* X = (const uint16_t*)x;
+    const uint16_t* Bp = (const uint16_t*)b;
+    const uint16_t* Rp = (const uint16_t*)r;
+    uint16_t* Yp = (uint16_t*)y;
+    int m = (int)M, n = (int)N, k = (int)K;
+    if (bits == 8 && mode == 0) mfma_dtype<8, false, false>(dt, geglu, st, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else if (bits == 8) mfma_dtype<8, true, false>(dt, geglu, st, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else if (mode == 0) mfma_dtype<4, false, false>(dt, geglu, st, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else mfma_dtype<4, true, false>(dt, geglu, st, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+  } else {
+    QWs q{(const uint8_t*)qw, (const void*)scales, (const void*)zeros, HB_F16, G, group, bits, mode};
+    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+    gemm_simt<<<grid, 256, 0, st>>>(dt, (const void*)x, ldx, nullptr, q, b, r, ldr, (void*)y, ldy, (int)M, (int)N,
+                                    (int)K, geglu ? 1 : 0);
+  }
+  check_launch("hb_qlinear");
+  HB_API_END
+}
+
+__global__ void qgather_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ scales,
+                               const uint16_t* __restrict__ zeros, int64_t V, int64_t K, int bits, int G, int group,
+                               int aff, const int32_t* __restrict__ ids, int64_t n, int dt_out,
+                               void* __restrict__ out) {
+  int64_t total = n * K;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = i / K, k = i - r * K;
+    int64_t id = ids[r];
+    id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+    int code;
+    if (bits == 8) {
+      uint8_t u = q[id * K + k];
+      code = aff ? (int)u : (int)(int8_t)u;
+    } else {
+      uint8_t u = q[id * (K / 2) + k / 2];
+      int v = (k & 1) ? (u >> 4) : (u & 15);
+      code = aff ? v : ((v ^ 8) - 8);
+    }
+    int64_t gi = id * G + k / group;
+    float s = f16_bits_to_f32(scales[gi]);
+    if (dt_out == HB_F16) {
+      f16 sh = (f16)s, qh = (f16)(float)code;
+      f16 w = aff ? __builtin_fmaf16(qh, sh, (f16)f16_bits_to_f32(zeros[gi])) : (f16)(qh * sh);
+      store_f(out, i, dt_out, (float)w);
+    } else {
+      // f32 with one rounding of the exact value (q*s is exact in f32)
+      float w = aff ? fmaf((float)code, s, f16_bits_to_f32(zeros[gi])) : (float)code * s;
+      store_f(out, i, dt_out, w);
+    }
+  }
+}
+
+extern "C" int hb_qgather(uintptr_t ctx, uintptr_t qw, uintptr_t scales, uintptr_t zeros, int64_t V, int64_t K,
+                          int bits, int group, int mode, uintptr_t ids, int64_t n, int dt_out, uintptr_t out) {
+  HB_API_BEGIN
+  HB_REQUIRE(bits == 8 || bits == 4, "hb_qgather: bits must be 8 or 4");
+  HB_REQUIRE(group > 0 && V > 0, "hb_qgather: bad shape");
+  HB_REQUIRE(mode == 0 || zeros, "hb_qgather: affine needs zeros");
+  int64_t total = n * K;
+  if (total == 0) return 0;
+  int G = (int)((K + group - 1) / group);
+  qgather_kernel<<<grid_for(total, 256), 256, 0, stream_of(ctx)>>>((const uint8_t*)qw, (const uint16_t*)scales,
+                                                                   (const uint16_t*)zeros, V, K, bits, G, group, mode,
+                                                                   (const int32_t*)ids, n, dt_out, (void*)out);
+  check_launch("hb_qgather");
+  HB_API_END
+}

@@ -1,0 +1,135 @@
+"""The ModernBERT encoder (packages/modernbert/src/index.ts) running
+unchanged on HipBackend: the tiny golden checkpoint stage by stage, the
+base-shape encoder at BASELINE config 0 against the CPU oracle, and batch
+independence of the config-3 encode (B=32, T=512, padded)."""
+import numpy as np
+import pytest
+
+from fixtures import arr, tiny
+from gpu_util import read32
+from laya_hip.host import HostTensor
+from laya_hip.modernbert import loadModernBert, parseModernBertConfig
+from oracle import cpu_ref as cr
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def b():
+    from laya_hip.backend import HipBackend
+    be = HipBackend(0)
+    yield be
+    be.destroy()
+
+
+def _getter(W, dtype):
+    def get(name):
+        if not name.startswith("encoder."):
+            return None
+        a = W.get(name[len("encoder."):])
+        if a is None:
+            return None
+        a = np.asarray(a, np.float32)
+        return HostTensor(dtype, a.shape, a.astype(np.float16) if dtype == "f16" else a)
+    return get
+
+
+@pytest.mark.parametrize("dtype,tol", [("f32", 1e-4), ("f16", 2e-2)])
+def test_tiny_encoder_stages(b, dtype, tol):
+    """modernbert.test.ts:65-117 on this backend; f16 at the reference's
+    f16 parity bar (0.02)."""
+    cfgj, W, act = tiny()
+    cfg = parseModernBertConfig(cfgj)
+    enc = loadModernBert(b, cfg, _getter(W, "f32"), dtype=dtype)
+    ids = arr(act["inputs"]["input_ids"])
+    mask = arr(act["inputs"]["attention_mask"])
+    B, L = ids.shape
+    stages = {}
+    out = enc.forward(ids, mask, B, L, onStage=lambda n, t: (stages.__setitem__(n, t), True)[1])
+    assert stages["final_norm"] is out
+    worst = 0.0
+    for name, t in stages.items():
+        want = arr(act["stages"]["embeddings" if name == "embeddings" else f"encoder.{name}"])
+        got = read32(b, t)
+        d = np.abs(got - want) - (tol + tol * np.abs(want))
+        worst = max(worst, float(np.max(np.abs(got - want))))
+        assert np.all(d <= 0), f"{name}: max abs err {np.max(np.abs(got - want)):.2e}"
+    print(f"tiny encoder {dtype}: max abs err {worst:.2e}")
+    pooled = read32(b, enc.embed(ids, mask, B, L))
+    fin = arr(act["stages"]["encoder.final_norm"])
+    for bb in range(B):
+        np.testing.assert_allclose(pooled[bb], fin[bb][mask[bb] != 0].mean(0), atol=max(tol, 1e-5))
+    for t in stages.values():
+        b.dispose(t)
+    enc.dispose()
+
+
+def base_weights(rng, H=768, I=1152, layers=22, V=50368):
+    """BASELINE config 0 weights: fp16 ~N(0, 0.02), LayerNorm gamma = 1."""
+    W = {"embeddings.tok_embeddings.weight": rng.normal(0, 0.02, (V, H)), "embeddings.norm.weight": np.ones(H),
+         "final_norm.weight": np.ones(H)}
+    for i in range(layers):
+        p = f"layers.{i}."
+        if i:
+            W[p + "attn_norm.weight"] = np.ones(H)
+        W[p + "attn.Wqkv.weight"] = rng.normal(0, 0.02, (3 * H, H))
+        W[p + "attn.Wo.weight"] = rng.normal(0, 0.02, (H, H))
+        W[p + "mlp_norm.weight"] = np.ones(H)
+        W[p + "mlp.Wi.weight"] = rng.normal(0, 0.02, (2 * I, H))
+        W[p + "mlp.Wo.weight"] = rng.normal(0, 0.02, (H, I))
+    return {k: np.asarray(v, np.float16).astype(np.float32) for k, v in W.items()}
+
+
+BASE_CFG = {"vocab_size": 50368, "hidden_size": 768, "intermediate_size": 1152, "num_hidden_layers": 22,
+            "num_attention_heads": 12, "local_attention": 128}
+
+
+def test_base_encoder_config0_matches_oracle(b):
+    """B=1, T=128, 22 layers, f16 on the GPU vs the f32 oracle (and the
+    oracle with f16 storage after every op)."""
+    rng = np.random.default_rng(0)
+    W = base_weights(rng)
+    cfg = parseModernBertConfig(BASE_CFG)
+    enc = loadModernBert(b, cfg, _getter(W, "f16"), dtype="f16")
+    ids = rng.integers(0, 50368, (1, 128)).astype(np.int32)
+    valid = np.ones((1, 128), np.uint8)
+    got = read32(b, enc.forward(ids, valid, 1, 128))
+    ocfg = cr.EncoderConfig.from_json(BASE_CFG)
+    ref32 = cr.encoder_forward(ocfg, W, ids, valid)
+    ref16 = cr.encoder_forward(ocfg, W, ids, valid, dtype="f16")
+    e32 = float(np.max(np.abs(got - ref32)))
+    e16 = float(np.max(np.abs(got - ref16)))
+    print(f"config0 encoder: max abs err vs f32 oracle {e32:.3e}, vs f16-storage oracle {e16:.3e}")
+    assert e32 <= 5e-2 and e16 <= 5e-2
+    pooled_got = got.mean(1)
+    pooled_ref = ref32.mean(1)
+    assert float(np.max(np.abs(pooled_got - pooled_ref))) <= 1e-2
+    enc.dispose()
+
+
+def test_config3_encode_batch_independence(b):
+    """B=32, T=512 with lengths uniform in [64, 512]: every sequence's valid
+    rows equal the same sequence encoded alone (rows are independent), and
+    one sequence matches the f32 oracle over 4 layers."""
+    rng = np.random.default_rng(1)
+    layers = 4
+    cfgj = dict(BASE_CFG, num_hidden_layers=layers)
+    W = base_weights(rng, layers=layers)
+    cfg = parseModernBertConfig(cfgj)
+    enc = loadModernBert(b, cfg, _getter(W, "f16"), dtype="f16")
+    B, T = 32, 512
+    lens = rng.integers(64, 513, B)
+    ids = rng.integers(0, 50368, (B, T)).astype(np.int32)
+    valid = (np.arange(T)[None, :] < lens[:, None]).astype(np.uint8)
+    full = read32(b, enc.forward(ids, valid, B, T))
+    for bb in (0, 5, 31):
+        one = read32(b, enc.forward(ids[bb:bb + 1], valid[bb:bb + 1], 1, T))
+        n = lens[bb]
+        np.testing.assert_array_equal(one[0, :n], full[bb, :n])
+    bb = 5
+    ref = cr.encoder_forward(cr.EncoderConfig.from_json(cfgj), W, ids[bb:bb + 1], valid[bb:bb + 1])
+    err = float(np.max(np.abs(full[bb, :lens[bb]] - ref[0, :lens[bb]])))
+    print(f"config3 (4 layers) sequence {bb} len {lens[bb]}: max abs err vs oracle {err:.3e}")
+    assert err <= 5e-2
+    assert np.isfinite(full).all()
+    enc.dispose()

@@ -1,0 +1,151 @@
+"""Linear-layer parity on the GPU (BASELINE configs 1 and 2).
+
+GEMM outputs of the MFMA kernels against the CPU oracle's f64-accumulated
+linear on the same rounded inputs: max-rel (max|y - r| / max|r|) <= 2e-3 for
+fp16 and 8e-3 for bf16; quantized weights <= 1e-2 against the oracle's
+dequantize-then-linear.  At M = 8192 / 16384 the oracle runs on a random
+subset of rows (rows are independent).  The one-hot test reads single
+dequantized weights back bit for bit: fl16(q*s + z), the value host
+dequantization uploads (backend-webgpu/test/quantized.test.ts:107-160)."""
+import numpy as np
+import pytest
+
+from gpu_util import max_rel, read32, rounded, to_host
+from laya_hip.host import HostQuantized, HostTensor, QuantizedLinearOptions, pack_quantized
+from oracle import cpu_ref as cr
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {"Wqkv": (2304, 768), "Wo": (768, 768), "Wi": (2304, 768), "WoMlp": (768, 1152)}
+MS = [128, 512, 2048, 8192, 16384]
+
+
+@pytest.fixture(scope="module")
+def b():
+    from laya_hip.backend import HipBackend
+    be = HipBackend(0)
+    yield be
+    be.destroy()
+
+
+def _rows(M, rng, n=384):
+    return np.arange(M) if M <= n else np.sort(rng.choice(M, n, replace=False))
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("name", list(SHAPES))
+@pytest.mark.parametrize("M", MS)
+def test_linear_config1(b, name, M, dtype):
+    N, K = SHAPES[name]
+    print(f"linear {name} M={M} {dtype}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    x = rounded(rng.standard_normal((M, K)), dtype)
+    w = rounded(rng.normal(0, 0.02, (N, K)), dtype)
+    X, Wt = b.fromHost(to_host(x, dtype)), b.fromHost(to_host(w, dtype))
+    geglu = name == "Wi"
+    if geglu:
+        y = b.geglu(b.linear(X, Wt))
+    else:
+        y = b.linear(X, Wt)
+    got = read32(b, y)
+    rows = _rows(M, rng)
+    lin = cr.linear(x[rows], w)
+    ref = cr.geglu(rounded(lin, dtype)) if geglu else lin
+    err = max_rel(got[rows], ref)
+    tol = 2e-3 if dtype == "f16" else 8e-3
+    assert err <= tol, f"{name} M={M} {dtype}: max-rel {err:.2e}"
+    for t in (X, Wt, y):
+        b.dispose(t)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_linear_bias_resid_ragged(b, dtype):
+    """Bias and residual epilogues, and ragged M / N / K (tails of every tile)."""
+    rng = np.random.default_rng(7)
+    for (M, N, K) in [(130, 200, 256), (37, 48, 72), (1, 3072, 1024), (333, 100, 256), (50, 96, 128), (4100, 770, 776)]:
+        x = rounded(rng.standard_normal((M, K)), dtype)
+        w = rounded(rng.normal(0, 0.05, (N, K)), dtype)
+        bias = rounded(rng.standard_normal(N), dtype)
+        r = rounded(rng.standard_normal((M, N)), dtype)
+        X, Wt, Bt, R = (b.fromHost(to_host(a, dtype)) for a in (x, w, bias, r))
+        y = b.add(R, b.linear(X, Wt, Bt))
+        got = read32(b, y)
+        lin = rounded(cr.linear(x, w, bias), dtype)
+        ref = r + lin
+        err = max_rel(got, ref)
+        assert err <= (2e-3 if dtype == "f16" else 8e-3), f"M={M} N={N} K={K}: {err:.2e}"
+        for t in (X, Wt, Bt, R, y):
+            b.dispose(t)
+    assert b.stats["linear_fused_resid"] > 0
+
+
+def test_linear_f32_path(b):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((70, 45)).astype(np.float32)
+    w = rng.standard_normal((33, 45)).astype(np.float32)
+    X, Wt = b.fromHost(to_host(x, "f32")), b.fromHost(to_host(w, "f32"))
+    got = read32(b, b.linear(X, Wt))
+    np.testing.assert_allclose(got, cr.linear(x, w), rtol=1e-5, atol=1e-5)
+
+
+def _quantized(rng, N, K, bits, g=64):
+    w = rounded(rng.normal(0, 0.02, (N, K)), "f16")
+    q, s, z = cr.quantize_matrix(w, N, K, bits, g, refine=bits == 4)
+    mode = "symmetric" if bits == 8 else "affine"
+    h = HostQuantized((N, K), bits, g, mode, pack_quantized(q, bits), HostTensor("f16", s.shape, s.view(np.float16)),
+                      HostTensor("f16", z.shape, z.view(np.float16)) if z is not None else None)
+    sf = s.view(np.float16).astype(np.float32)
+    zf = z.view(np.float16).astype(np.float32) if z is not None else None
+    return h, q, sf, zf
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("name", list(SHAPES))
+@pytest.mark.parametrize("M", [512, 8192])
+def test_qlinear_config2(b, name, M, bits):
+    from laya_hip import compose as C
+    N, K = SHAPES[name]
+    print(f"qlinear {name} M={M} q{bits}", flush=True)
+    rng = np.random.default_rng(M + N + bits)
+    h, q, sf, zf = _quantized(rng, N, K, bits)
+    x = rounded(rng.standard_normal((M, K)), "f16")
+    X = b.fromHost(to_host(x, "f16"))
+    Q = C.upload_quantized(b, h, "f16")
+    assert Q.native
+    geglu = name == "Wi"
+    y = C.quantized_linear(b, X, Q)
+    if geglu:
+        y = b.geglu(y)
+    got = read32(b, y)
+    rows = _rows(M, rng)
+    lin = cr.quantized_linear(x[rows], q, sf, zf, 64, dtype="f16")
+    ref = cr.geglu(rounded(lin, "f16")) if geglu else lin
+    err = max_rel(got[rows], ref)
+    assert err <= 1e-2, f"{name} M={M} q{bits}: max-rel {err:.2e}"
+    C.dispose_quantized(b, Q)
+    b.dispose(X)
+
+
+@pytest.mark.parametrize("bits,mode", [(8, "symmetric"), (4, "affine"), (8, "affine"), (4, "symmetric")])
+def test_qlinear_one_hot_reads_exact_weights(b, bits, mode):
+    """x = identity rows: y[k, n] = dequant(W)[n, k] must equal fl16(q*s + z)
+    exactly (subnormal scales included)."""
+    from laya_hip import compose as C
+    rng = np.random.default_rng(bits)
+    N, K, g = 64, 128, 32
+    lo, hi = {(8, "symmetric"): (-127, 127), (8, "affine"): (0, 255), (4, "symmetric"): (-8, 7),
+              (4, "affine"): (0, 15)}[(bits, mode)]
+    q = rng.integers(lo, hi + 1, (N, K))
+    s16 = rng.uniform(1e-6, 0.05, (N, K // g)).astype(np.float16)
+    s16[0, 0] = np.float16(3e-7)  # subnormal
+    z16 = rng.uniform(-0.1, 0.1, (N, K // g)).astype(np.float16)
+    h = HostQuantized((N, K), bits, g, mode, pack_quantized(q, bits), HostTensor("f16", s16.shape, s16),
+                      HostTensor("f16", z16.shape, z16) if mode == "affine" else None)
+    Q = C.upload_quantized(b, h, "f16")
+    assert Q.native
+    X = b.fromHost(to_host(np.eye(K, dtype=np.float32), "f16"))
+    got = b.read(C.quantized_linear(b, X, Q)).data.astype(np.float16).view(np.uint16)
+    want = cr.dequant_exact_f16(q, s16.astype(np.float32), z16.astype(np.float32) if mode == "affine" else None, g)
+    np.testing.assert_array_equal(got, want.T)
+    E = C.quantized_embedding(b, Q, b.fromHost(HostTensor("i32", (N,), np.arange(N, dtype=np.int32))))
+    np.testing.assert_array_equal(b.read(E).data.view(np.uint16), want)
