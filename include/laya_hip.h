@@ -188,12 +188,22 @@ int hb_rope(uintptr_t ctx, int dt_x, uintptr_t x, const int64_t* xs, int dt_y, u
  * q [B,H,Lq,D], k/v [B,H,Lk,D] and o [B,H,Lq,D] by element strides (4
  * each, last must be 1 for the MFMA path); mask is bool (1 byte) addressed
  * by ms[4] over [B,H,Lq,Lk] (0 = broadcast), or 0 for none.
+ * mask_info: 0, or the summary hb_sdpa_mask_info wrote for this very mask
+ * (and B, Lq, Lk), so a mask reused by many layers is summarised once.
  * rope_q / rope_k: when > 0, q (k) is first rotated by RoPE with that base
  * and rounded to dt, exactly as a preceding Backend.rope would
  * (modernbert/src/index.ts:351). */
 int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks, uintptr_t v,
-            const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t o, const int64_t* os, int64_t B, int64_t H,
-            int64_t Lq, int64_t Lk, int64_t D, float scale, double rope_q, double rope_k);
+            const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info, uintptr_t o, const int64_t* os,
+            int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, float scale, double rope_q, double rope_k);
+/* Size of a mask summary for (B, Lq, Lk). */
+int hb_sdpa_mask_info_bytes(int64_t B, int64_t Lq, int64_t Lk, size_t* bytes);
+/* Summarises a bool attention mask (strides ms[4] over [B,H,Lq,Lk], head
+ * stride ignored) into `info`: for every (batch, 128-query, 64-key) tile
+ * whether no key, every key or some keys are visible.  Enqueued on the
+ * context's stream; `info` must stay alive while hb_sdpa calls use it. */
+int hb_sdpa_mask_info(uintptr_t ctx, uintptr_t mask, const int64_t* ms, int64_t B, int64_t Lq, int64_t Lk,
+                      uintptr_t info);
 
 /* gelu(value) * gate over x [rows, 2F] (row stride ldx) -> y [rows, F].
  * Backend.geglu (index.ts:240-241), compose.ts:86-93. */

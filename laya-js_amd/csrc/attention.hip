@@ -37,49 +37,54 @@ static S4 s4(const int64_t* p) {
 
 constexpr int kBQ = 128;  // queries per block
 constexpr int kBK = 64;   // keys per tile
+constexpr int kMaxKeyTiles = 1024;  // Lk <= 65536 on the MFMA path
 
-// ------------------------------------------------------------------ mask pre-pass
+// ------------------------------------------------------------------ mask summary
 
-// ranges[b * nqt + qt] = [first, last + 1) key TILE with any visible key for
-// any query of the tile (any head).
-__global__ __launch_bounds__(256) void mask_range_kernel(const uint8_t* __restrict__ mask, S4 ms, int H, int Lq,
-                                                         int Lk, int nqt, int2* __restrict__ ranges) {
-  __shared__ int lo, hi;
-  const int qt = blockIdx.x, b = blockIdx.y;
-  if (threadIdx.x == 0) {
-    lo = Lk;
-    hi = -1;
-  }
-  __syncthreads();
-  const int q0 = qt * kBQ;
-  const int nq = min(kBQ, Lq - q0);
-  const int hn = ms.s[1] == 0 ? 1 : H;
-  const int qn = ms.s[2] == 0 ? 1 : nq;
-  int mylo = Lk, myhi = -1;
-  const int64_t total = (int64_t)hn * qn * Lk;
-  for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
-    int k = (int)(i % Lk);
-    int64_t rest = i / Lk;
-    int q = (int)(rest % qn), h = (int)(rest / qn);
-    if (mask[b * ms.s[0] + h * ms.s[1] + (int64_t)(q0 + q) * ms.s[2] + k * ms.s[3]]) {
-      mylo = min(mylo, k);
-      myhi = max(myhi, k);
+// Class of every (batch, 128-query tile, 64-key tile) block of a bool mask:
+// 0 = no visible key (skipped), 1 = every key visible (no mask reads),
+// 2 = mixed or running past Lk (per-element mask).  Computed once per mask
+// tensor and reused by every layer that attends with it.
+__global__ __launch_bounds__(256) void mask_class_kernel(const uint8_t* __restrict__ mask, S4 ms, int Lq, int Lk,
+                                                         int nqt, int nkt, uint8_t* __restrict__ cls, int vec) {
+  const int kt = blockIdx.x, qt = blockIdx.y, b = blockIdx.z;
+  const int q0 = qt * kBQ, k0 = kt * kBK;
+  const int nq = min(kBQ, Lq - q0), nk = min(kBK, Lk - k0);
+  const int qn = ms.s[2] == 0 ? 1 : nq;  // a [B,1,1,L] mask has one row for every query
+  int any = 0, all = 1;
+  if (vec && nk == kBK) {
+    // 16-byte rows chunks: qn rows x 4 chunks
+    for (int i = threadIdx.x; i < qn * 4; i += blockDim.x) {
+      int q = i >> 2, c = i & 3;
+      uint4v w = *(const uint4v*)(mask + b * ms.s[0] + (int64_t)(q0 + q) * ms.s[2] + k0 + c * 16);
+      // bytes are 0/1: any byte set <=> word != 0; all set <=> every byte == 1
+      uint32_t o = w.x | w.y | w.z | w.w, a = w.x & w.y & w.z & w.w;
+      any |= o != 0;
+      all &= a == 0x01010101u;
+    }
+  } else {
+    for (int i = threadIdx.x; i < qn * nk; i += blockDim.x) {
+      int q = i / nk, k = i - q * nk;
+      uint8_t m = mask[b * ms.s[0] + (int64_t)(q0 + q) * ms.s[2] + (int64_t)(k0 + k) * ms.s[3]];
+      any |= m != 0;
+      all &= m != 0;
     }
   }
-  atomicMin(&lo, mylo);
-  atomicMax(&hi, myhi);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int2 r;
-    if (hi < 0) {
-      r.x = 0;
-      r.y = 0;
-    } else {
-      r.x = lo / kBK;
-      r.y = hi / kBK + 1;
-    }
-    ranges[b * nqt + qt] = r;
-  }
+  any = __syncthreads_or(any);
+  all = __syncthreads_and(all);
+  if (threadIdx.x == 0) cls[((int64_t)b * nqt + qt) * nkt + kt] = !any ? 0 : (all && nk == kBK ? 1 : 2);
+}
+
+static size_t mask_info_bytes(int64_t B, int64_t Lq, int64_t Lk) {
+  int64_t nqt = (Lq + kBQ - 1) / kBQ, nkt = (Lk + kBK - 1) / kBK;
+  return (size_t)(B * nqt * nkt);
+}
+
+static void launch_mask_info(hipStream_t st, const uint8_t* mask, const S4& ms, int64_t B, int64_t Lq, int64_t Lk,
+                             uint8_t* info) {
+  int nqt = (int)((Lq + kBQ - 1) / kBQ), nkt = (int)((Lk + kBK - 1) / kBK);
+  int vec = ms.s[3] == 1 && ((uintptr_t)mask % 16 == 0) && ms.s[0] % 16 == 0 && ms.s[2] % 16 == 0;
+  mask_class_kernel<<<dim3(nkt, nqt, (unsigned)B), 256, 0, st>>>(mask, ms, (int)Lq, (int)Lk, nqt, nkt, info, vec);
 }
 
 // ------------------------------------------------------------------ MFMA kernel (D = 64)
@@ -102,35 +107,54 @@ __device__ __forceinline__ uint32_t fromf(float v) {
   return BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
 }
 
+// Two f32 values packed as 16-bit (f16: v_cvt_pk_f16_f32; bf16: RNE).
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (BF16) {
+    return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+  } else {
+    typedef float float2v __attribute__((ext_vector_type(2)));
+    half2v h = __builtin_convertvector((float2v){a, b}, half2v);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+}
+
 __device__ __forceinline__ int qk_swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
 constexpr int kVtLd = 72;  // row stride (elements) of V^T in LDS
 
-// Loads row `row` (chunks c and c + 4, i.e. d in [8c, 8c+8) and the matching
-// rotation partners d + 32) of a [L, 64] operand, rotating by RoPE at
-// position `pos` when `tab` is set; writes both chunks to LDS.
-template <bool BF16>
-__device__ __forceinline__ void stage_pair(const uint16_t* __restrict__ src, bool valid, int c,
-                                           const float2* __restrict__ tab, int pos, uint16_t* lds, int row) {
-  uint4v lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+// Raw chunks c and c + 4 (d in [8c, 8c+8) and the rotation partners d + 32)
+// of one row of a [L, 64] operand; zero when the row is out of range.
+__device__ __forceinline__ void load_pair(const uint16_t* __restrict__ src, bool valid, int c, uint4v& lo,
+                                          uint4v& hi) {
+  lo = uint4v{0, 0, 0, 0};
+  hi = uint4v{0, 0, 0, 0};
   if (valid) {
     lo = *(const uint4v*)(src + c * 8);
     hi = *(const uint4v*)(src + 32 + c * 8);
-    if (tab != nullptr) {
-      const float2* t = tab + pos * 32 + c * 8;
-      uint32_t* l = (uint32_t*)&lo;
-      uint32_t* h = (uint32_t*)&hi;
+  }
+}
+
+// Rotates a loaded chunk pair by RoPE at position `pos` (when `tab` is set),
+// rounding to the storage type like a separate Backend.rope, and writes it
+// to the swizzled [rows][64] LDS tile.
+template <bool BF16>
+__device__ __forceinline__ void store_pair(uint4v lo, uint4v hi, bool valid, int c, const float2* __restrict__ tab,
+                                           int pos, uint16_t* lds, int row) {
+  if (valid && tab != nullptr) {
+    const float2* t = tab + pos * 32 + c * 8;
+    uint32_t* l = (uint32_t*)&lo;
+    uint32_t* h = (uint32_t*)&hi;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        float2 c0 = t[2 * e], c1 = t[2 * e + 1];
-        float x0a = tof<BF16>(l[e] & 0xffff), x0b = tof<BF16>(l[e] >> 16);
-        float x1a = tof<BF16>(h[e] & 0xffff), x1b = tof<BF16>(h[e] >> 16);
-        uint32_t oa = fromf<BF16>(pin_f32(fmaf(-x1a, c0.y, x0a * c0.x)));
-        uint32_t ob = fromf<BF16>(pin_f32(fmaf(-x1b, c1.y, x0b * c1.x)));
-        uint32_t pa = fromf<BF16>(pin_f32(fmaf(x0a, c0.y, x1a * c0.x)));
-        uint32_t pb = fromf<BF16>(pin_f32(fmaf(x0b, c1.y, x1b * c1.x)));
-        l[e] = oa | (ob << 16);
-        h[e] = pa | (pb << 16);
-      }
+    for (int e = 0; e < 4; e++) {
+      float2 c0 = t[2 * e], c1 = t[2 * e + 1];
+      float x0a = tof<BF16>(l[e] & 0xffff), x0b = tof<BF16>(l[e] >> 16);
+      float x1a = tof<BF16>(h[e] & 0xffff), x1b = tof<BF16>(h[e] >> 16);
+      uint32_t oa = fromf<BF16>(pin_f32(fmaf(-x1a, c0.y, x0a * c0.x)));
+      uint32_t ob = fromf<BF16>(pin_f32(fmaf(-x1b, c1.y, x0b * c1.x)));
+      uint32_t pa = fromf<BF16>(pin_f32(fmaf(x0a, c0.y, x1a * c0.x)));
+      uint32_t pb = fromf<BF16>(pin_f32(fmaf(x0b, c1.y, x1b * c1.x)));
+      l[e] = oa | (ob << 16);
+      h[e] = pa | (pb << 16);
     }
   }
   *(uint4v*)(lds + qk_swz(row, c)) = lo;
@@ -141,26 +165,45 @@ template <bool BF16>
 __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q, S4 qs, const uint16_t* __restrict__ K,
                                                  S4 ks, const uint16_t* __restrict__ V, S4 vs,
                                                  const uint8_t* __restrict__ mask, S4 ms, int mask_vec,
-                                                 const int2* __restrict__ ranges, uint16_t* __restrict__ O, S4 os,
+                                                 const uint8_t* __restrict__ cls, uint16_t* __restrict__ O, S4 os,
                                                  int Lq, int Lk, float scale_log2, const float2* __restrict__ tabq,
                                                  const float2* __restrict__ tabk) {
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ * 64];
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kBK * 64];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[64 * kVtLd];
+  __shared__ uint8_t cls_row[kMaxKeyTiles];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
   const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int nqt = gridDim.x, nkt = (Lk + kBK - 1) / kBK;
   const int q0 = qt * kBQ;
   const uint16_t* Qb = Q + b * qs.s[0] + h * qs.s[1];
   const uint16_t* Kb = K + b * ks.s[0] + h * ks.s[1];
   const uint16_t* Vb = V + b * vs.s[0] + h * vs.s[1];
+  // tile classes of this (b, query tile): 0 skip, 1 all visible, 2 per-element
+  // mask / key bound; staged in LDS once (the host caps nkt at kMaxKeyTiles)
+  for (int t = tid; t < nkt; t += 256) {
+    uint8_t c;
+    if (cls != nullptr) c = cls[((int64_t)b * nqt + qt) * nkt + t];
+    else if (mask != nullptr) c = 2;
+    else c = (t + 1) * kBK <= Lk ? 1 : 2;
+    cls_row[t] = c;
+  }
+  auto tile_class = [&](int kt) -> int { return cls_row[kt]; };
+  auto next_tile = [&](int kt) -> int {
+    kt++;
+    while (kt < nkt && tile_class(kt) == 0) kt++;
+    return kt;
+  };
 
   // ---- stage Q (rotated) and build this wave's B fragments of Q^T
   for (int t = tid; t < kBQ * 4; t += 256) {
     int r = t >> 2, c = t & 3;
     int q = q0 + r;
-    stage_pair<BF16>(Qb + (int64_t)q * qs.s[2], q < Lq, c, tabq, q, Qs, r);
+    uint4v lo, hi;
+    load_pair(Qb + (int64_t)q * qs.s[2], q < Lq, c, lo, hi);
+    store_pair<BF16>(lo, hi, q < Lq, c, tabq, q, Qs, r);
   }
   __syncthreads();
   uint4v qf[2][2];
@@ -169,13 +212,6 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
 #pragma unroll
     for (int s = 0; s < 2; s++) qf[qb][s] = *(const uint4v*)(Qs + qk_swz(wave * 32 + qb * 16 + li, s * 4 + g));
 
-  int kt0 = 0, kt1 = (Lk + kBK - 1) / kBK;
-  if (ranges != nullptr) {
-    int2 r = ranges[b * gridDim.x + qt];
-    kt0 = r.x;
-    kt1 = r.y;
-  }
-
   float4v o[2][4];
 #pragma unroll
   for (int qb = 0; qb < 2; qb++)
@@ -183,31 +219,68 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
     for (int d = 0; d < 4; d++) o[qb][d] = float4v{0.f, 0.f, 0.f, 0.f};
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
 
-  for (int kt = kt0; kt < kt1; kt++) {
+  // this thread's share of a K tile (row kr, chunk pair kc) and V tile
+  // (key pair vj, chunk vc), prefetched into registers one tile ahead
+  const int kr = tid >> 2, kc = tid & 3;
+  const int vc = tid & 7, vj = 2 * (tid >> 3);
+  uint4v klo, khi, va, vb;
+  auto prefetch = [&](int kt) {
     const int k0 = kt * kBK;
-    __syncthreads();  // previous tile's K / V^T reads are done
-    {  // K tile (rotated): 64 rows x 4 chunk pairs = one task per thread
-      int r = tid >> 2, c = tid & 3;
-      int kk = k0 + r;
-      stage_pair<BF16>(Kb + (int64_t)kk * ks.s[2], kk < Lk, c, tabk, kk, Ks, r);
-    }
-    {  // V tile, transposed into V^T [d][key]: thread = (key pair, chunk)
-      int c = tid & 7, jp = tid >> 3;
-      int j0 = 2 * jp, kk = k0 + j0;
-      uint4v a = {0, 0, 0, 0}, bb = {0, 0, 0, 0};
-      if (kk < Lk) a = *(const uint4v*)(Vb + (int64_t)kk * vs.s[2] + c * 8);
-      if (kk + 1 < Lk) bb = *(const uint4v*)(Vb + (int64_t)(kk + 1) * vs.s[2] + c * 8);
-      const uint32_t* pa = (const uint32_t*)&a;
-      const uint32_t* pb = (const uint32_t*)&bb;
+    load_pair(Kb + (int64_t)(k0 + kr) * ks.s[2], k0 + kr < Lk, kc, klo, khi);
+    va = uint4v{0, 0, 0, 0};
+    vb = uint4v{0, 0, 0, 0};
+    if (k0 + vj < Lk) va = *(const uint4v*)(Vb + (int64_t)(k0 + vj) * vs.s[2] + vc * 8);
+    if (k0 + vj + 1 < Lk) vb = *(const uint4v*)(Vb + (int64_t)(k0 + vj + 1) * vs.s[2] + vc * 8);
+  };
+
+  int kt = next_tile(-1);
+  if (kt < nkt) prefetch(kt);
+  while (kt < nkt) {
+    const int k0 = kt * kBK;
+    const int cl = tile_class(kt);
+    __syncthreads();  // the previous tile's K / V^T reads are done
+    store_pair<BF16>(klo, khi, k0 + kr < Lk, kc, tabk, k0 + kr, Ks, kr);
+    {
+      const uint32_t* pa = (const uint32_t*)&va;
+      const uint32_t* pb = (const uint32_t*)&vb;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         uint32_t lo = (pa[e] & 0xffff) | (pb[e] << 16);
         uint32_t hi = (pa[e] >> 16) | (pb[e] & 0xffff0000u);
-        *(uint32_t*)(Vt + (c * 8 + 2 * e) * kVtLd + j0) = lo;
-        *(uint32_t*)(Vt + (c * 8 + 2 * e + 1) * kVtLd + j0) = hi;
+        *(uint32_t*)(Vt + (vc * 8 + 2 * e) * kVtLd + vj) = lo;
+        *(uint32_t*)(Vt + (vc * 8 + 2 * e + 1) * kVtLd + vj) = hi;
       }
     }
     __syncthreads();
+
+    // mask bytes of this tile (issued before the next tile's prefetch, so
+    // waiting for them does not wait for the prefetch)
+    uint2v mw[2][2];
+    if (cl == 2 && mask != nullptr) {
+#pragma unroll
+      for (int qb = 0; qb < 2; qb++) {
+        const int q = q0 + wave * 32 + qb * 16 + li;
+        const uint8_t* mrow = mask + b * ms.s[0] + (int64_t)(q < Lq ? q : 0) * ms.s[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          const int kbase = k0 + 32 * t + 8 * g;
+          if (mask_vec && kbase + 8 <= Lk) {
+            mw[qb][t] = *(const uint2v*)(mrow + kbase);
+          } else {
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+              uint32_t bit = (kbase + e < Lk) ? (mrow[(int64_t)(kbase + e) * ms.s[3]] != 0) : 0u;
+              if (e < 4) w0 |= bit << (8 * e);
+              else w1 |= bit << (8 * (e - 4));
+            }
+            mw[qb][t] = uint2v{w0, w1};
+          }
+        }
+      }
+    }
+    const int nk = next_tile(kt);
+    if (nk < nkt) prefetch(nk);
 
     // ---- S^T = K . Q^T over 4 key blocks; block kb row i holds key
     // 32*(kb/2) + 8*(i/4) + (i%4) + 4*(kb%2) so a lane's 8 keys are contiguous
@@ -225,47 +298,36 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
       }
     }
 
-    // ---- mask, online softmax, P fragments
+    // ---- mask, online softmax (log2 domain, scale folded into one fma), P fragments
+    const bool in_range = k0 + kBK <= Lk;
     uint4v pf[2][2];
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
-      const int q = q0 + wave * 32 + qb * 16 + li;
       float sv[2][8];
       float mx = -INFINITY;
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         const int kbase = k0 + 32 * t + 8 * g;  // this lane's 8 contiguous keys
-        uint8_t mb[8];
-        if (mask != nullptr) {
-          const uint8_t* mp = mask + b * ms.s[0] + (int64_t)(q < Lq ? q : 0) * ms.s[2] + kbase * ms.s[3];
-          if (mask_vec && kbase + 8 <= Lk) {
-            uint2v w = *(const uint2v*)mp;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              mb[e] = (w.x >> (8 * e)) & 0xff;
-              mb[4 + e] = (w.y >> (8 * e)) & 0xff;
-            }
-          } else {
-#pragma unroll
-            for (int e = 0; e < 8; e++) mb[e] = (kbase + e < Lk) ? mp[e * ms.s[3]] : 0;
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; e++) mb[e] = 1;
-        }
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-          float s = (e < 4 ? st[qb][2 * t][e] : st[qb][2 * t + 1][e - 4]) * scale_log2;
-          bool vis = mb[e] != 0 && (kbase + e) < Lk;
+          const float s = e < 4 ? st[qb][2 * t][e] : st[qb][2 * t + 1][e - 4];
+          bool vis = true;
+          if (cl == 2) {
+            if (mask != nullptr) {
+              const uint32_t w = e < 4 ? mw[qb][t].x : mw[qb][t].y;
+              vis = ((w >> (8 * (e & 3))) & 0xffu) != 0;
+            }
+            if (!in_range) vis = vis && (kbase + e) < Lk;
+          }
           sv[t][e] = vis ? s : -INFINITY;
           mx = fmaxf(mx, sv[t][e]);
         }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m[qb], mx);
-      const float muse = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = exp2f(m[qb] - muse);
+      const float mnew = fmaxf(m[qb], mx);                       // raw (unscaled) row max
+      const float mc = mnew == -INFINITY ? 0.f : mnew * scale_log2;
+      const float alpha = __builtin_amdgcn_exp2f(m[qb] * scale_log2 - mc);
       m[qb] = mnew;
       float psum = 0.f;
 #pragma unroll
@@ -273,15 +335,19 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
         uint32_t pk[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-          float p0 = exp2f(sv[t][e] - muse), p1 = exp2f(sv[t][e + 1] - muse);
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[t][e], scale_log2, -mc));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[t][e + 1], scale_log2, -mc));
           psum += p0 + p1;
-          pk[e >> 1] = fromf<BF16>(p0) | (fromf<BF16>(p1) << 16);
+          pk[e >> 1] = pack2<BF16>(p0, p1);
         }
         pf[qb][t] = uint4v{pk[0], pk[1], pk[2], pk[3]};
       }
       l[qb] = l[qb] * alpha + psum;
+      // rescale O only when some row max of this wave moved
+      if (!__all(alpha == 1.0f)) {
 #pragma unroll
-      for (int d = 0; d < 4; d++) o[qb][d] *= alpha;
+        for (int d = 0; d < 4; d++) o[qb][d] *= alpha;
+      }
     }
 
     // ---- O^T += V^T . P^T
@@ -294,6 +360,7 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
         for (int qb = 0; qb < 2; qb++) o[qb][d] = mfma16<BF16>(vf, pf[qb][t], o[qb][d]);
       }
     }
+    kt = nk;
   }
 
   // ---- normalise and store (lane: one query, d = 16*dblk + 4g + 0..3)
@@ -382,10 +449,29 @@ __global__ __launch_bounds__(64) void sdpa_simt(int dt, const void* __restrict__
 
 using namespace hb;
 
+extern "C" int hb_sdpa_mask_info_bytes(int64_t B, int64_t Lq, int64_t Lk, size_t* bytes) {
+  HB_API_BEGIN
+  HB_REQUIRE(bytes && B >= 0 && Lq >= 0 && Lk >= 0, "hb_sdpa_mask_info_bytes: bad arguments");
+  *bytes = mask_info_bytes(B, Lq, Lk);
+  HB_API_END
+}
+
+extern "C" int hb_sdpa_mask_info(uintptr_t ctx, uintptr_t mask, const int64_t* ms, int64_t B, int64_t Lq, int64_t Lk,
+                                 uintptr_t info) {
+  HB_API_BEGIN
+  HB_REQUIRE(mask && ms && info, "hb_sdpa_mask_info: null argument");
+  HB_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && B < 65536 && Lq < (1 << 30) && Lk < (1 << 30),
+             "hb_sdpa_mask_info: bad shape");
+  if (B == 0 || Lq == 0 || Lk == 0) return 0;
+  launch_mask_info(stream_of(ctx), (const uint8_t*)mask, s4(ms), B, Lq, Lk, (uint8_t*)info);
+  check_launch("hb_sdpa_mask_info");
+  HB_API_END
+}
+
 extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
-                       uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t o,
-                       const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, float scale,
-                       double rope_q, double rope_k) {
+                       uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info,
+                       uintptr_t o, const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
+                       float scale, double rope_q, double rope_k) {
   HB_API_BEGIN
   HB_REQUIRE(dt == HB_F32 || dt == HB_F16 || dt == HB_BF16, "hb_sdpa: dtype must be f32, f16 or bf16");
   HB_REQUIRE(qs && ks && vs && os, "hb_sdpa: null strides");
@@ -395,39 +481,42 @@ extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, ui
   if (B == 0 || H == 0 || Lq == 0) return 0;
   HB_REQUIRE((rope_q <= 0 && rope_k <= 0) || D % 2 == 0, "hb_sdpa: rope needs an even head dim");
   hipStream_t st = stream_of(ctx);
-  int64_t Lt = Lq > Lk ? Lq : Lk;
   const float2* tq = rope_q > 0 ? (const float2*)rope_table(ctx, Lq, D, rope_q) : nullptr;
   const float2* tk = rope_k > 0 ? (const float2*)rope_table(ctx, Lk, D, rope_k) : nullptr;
-  (void)Lt;
   S4 Qs = s4(qs), Ks = s4(ks), Vs = s4(vs), Ms = s4(ms), Os = s4(os);
   bool fast = (dt == HB_F16 || dt == HB_BF16) && D == 64 && qs[3] == 1 && ks[3] == 1 && vs[3] == 1 && os[3] == 1 &&
               q % 16 == 0 && k % 16 == 0 && v % 16 == 0 && o % 8 == 0 && qs[2] % 8 == 0 && ks[2] % 8 == 0 &&
               vs[2] % 8 == 0 && qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 &&
               vs[0] % 8 == 0 && vs[1] % 8 == 0 && os[0] % 4 == 0 && os[1] % 4 == 0 && os[2] % 4 == 0 &&
-              (mask == 0 || ms[1] == 0);
+              (mask == 0 || ms[1] == 0) && (Lk + kBK - 1) / kBK <= kMaxKeyTiles;
   if (fast) {
     int nqt = (int)((Lq + kBQ - 1) / kBQ);
-    int2* ranges = nullptr;
+    uint8_t* info = (uint8_t*)mask_info;
+    uint8_t* tmp = nullptr;
     int mask_vec = 0;
     if (mask) {
-      ranges = (int2*)pool_alloc(ctx, sizeof(int2) * (size_t)(B * nqt));
-      mask_range_kernel<<<dim3(nqt, (unsigned)B), 256, 0, st>>>((const uint8_t*)mask, Ms, (int)H, (int)Lq, (int)Lk,
-                                                                 nqt, ranges);
-      check_launch("hb_sdpa(mask ranges)");
+      if (!info) {
+        tmp = (uint8_t*)pool_alloc(ctx, mask_info_bytes(B, Lq, Lk));
+        launch_mask_info(st, (const uint8_t*)mask, Ms, B, Lq, Lk, tmp);
+        check_launch("hb_sdpa(mask info)");
+        info = tmp;
+      }
       mask_vec = ms[3] == 1 && mask % 8 == 0 && ms[0] % 8 == 0 && ms[2] % 8 == 0;
+    } else {
+      info = nullptr;
     }
     const float sl2 = scale * 1.4426950408889634f;
     dim3 grid(nqt, (unsigned)H, (unsigned)B);
     if (dt == HB_F16)
       sdpa_mfma<false><<<grid, 256, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
-                                             (const uint8_t*)mask, Ms, mask_vec, ranges, (uint16_t*)o, Os, (int)Lq,
+                                             (const uint8_t*)mask, Ms, mask_vec, info, (uint16_t*)o, Os, (int)Lq,
                                              (int)Lk, sl2, tq, tk);
     else
       sdpa_mfma<true><<<grid, 256, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
-                                            (const uint8_t*)mask, Ms, mask_vec, ranges, (uint16_t*)o, Os, (int)Lq,
+                                            (const uint8_t*)mask, Ms, mask_vec, info, (uint16_t*)o, Os, (int)Lq,
                                             (int)Lk, sl2, tq, tk);
     check_launch("hb_sdpa");
-    if (ranges) pool_free(ctx, ranges);
+    if (tmp) pool_free(ctx, tmp);
   } else {
     size_t lds = sizeof(float) * (size_t)(Lk + D);
     HB_REQUIRE(lds <= 160 * 1024, "hb_sdpa: sequence too long for the generic kernel");

@@ -116,6 +116,44 @@ struct QW {  // quantized weight operand
   int group;  // values per group
 };
 
+// Copies a [BM][BNO] 16-bit tile staged in LDS to Y with 16-byte coalesced
+// stores; with a residual, y = round(tile + resid) (linear, then add).
+template <bool BF16, int BM, int BNO, int NT>
+__device__ __forceinline__ void write_tile(const uint16_t* Cs, int m0, int n0, int M, int N,
+                                           const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
+                                           int64_t ldy) {
+  constexpr int CPR = BNO / 8;  // chunks per row
+  for (int q = threadIdx.x; q < BM * CPR; q += NT) {
+    const int r = q / CPR, c = q % CPR;
+    const int gm = m0 + r, gn = n0 + c * 8;
+    if (gm >= M || gn >= N) continue;
+    uint4v v = *(const uint4v*)(Cs + r * BNO + c * 8);
+    if (gn + 8 <= N) {
+      if (R != nullptr) {
+        uint4v rv = *(const uint4v*)(R + (int64_t)gm * ldr + gn);
+        uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t rr[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          uint16_t lo = from_f<BF16>(to_f<BF16>(vv[e] & 0xffff) + to_f<BF16>(rr[e] & 0xffff));
+          uint16_t hi = from_f<BF16>(to_f<BF16>(vv[e] >> 16) + to_f<BF16>(rr[e] >> 16));
+          vv[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        v = uint4v{vv[0], vv[1], vv[2], vv[3]};
+      }
+      *(uint4v*)(Y + (int64_t)gm * ldy + gn) = v;
+    } else {
+      uint16_t vs[8];
+      __builtin_memcpy(vs, &v, 16);
+      for (int e = 0; e < 8 && gn + e < N; e++) {
+        uint16_t o = vs[e];
+        if (R != nullptr) o = from_f<BF16>(to_f<BF16>(o) + to_f<BF16>(R[(int64_t)gm * ldr + gn + e]));
+        Y[(int64_t)gm * ldy + gn + e] = o;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ MFMA kernel
 
 template <int BM, int BN, int WM, int WN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
@@ -292,37 +330,232 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
   }
   __syncthreads();
 
-  // ---- coalesced write-out (16-byte chunks), residual added here
-  constexpr int CPR = BNO / 8;  // chunks per row
-  for (int q = tid; q < BM * CPR; q += NT) {
-    const int r = q / CPR, c = q % CPR;
-    const int gm = m0 + r, gn = n0 + c * 8;
-    if (gm >= M || gn >= N) continue;
-    uint4v v = *(const uint4v*)(Cs + r * BNO + c * 8);
-    if (gn + 8 <= N) {
-      if (R != nullptr) {
-        uint4v rv = *(const uint4v*)(R + (int64_t)gm * ldr + gn);
-        uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-        uint32_t rr[4] = {rv.x, rv.y, rv.z, rv.w};
+  write_tile<BF16, BM, BNO, NT>(Cs, m0, n0, M, N, R, ldr, Y, ldy);
+}
+
+// ------------------------------------------------------------------ large-M MFMA kernel
+
+template <bool BF16>
+__device__ __forceinline__ float16v mfma32(const uint4v& a, const uint4v& b, float16v c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                  0, 0);
+  }
+}
+
+// 256 x BN output tile, four waves stacked along M: each wave owns 64 rows
+// and every column of the tile as 2 x (BN/32) blocks of v_mfma_f32_32x32x16
+// (on gfx950 the 32x32 MFMA runs at twice the rate of the 16x16x32 one, and
+// reaches it from a single wave per SIMD).  A wave's A rows are private, so
+// they go from global memory straight into MFMA A-operand registers; only
+// the weight tile is shared, through double-buffered LDS.  Loads run two K
+// stages ahead of the MFMAs (three A and two W register sets rotating by
+// name), so global latency hides behind two stages of MFMA work.  BN = 192
+// makes every ModernBERT-base linear at M = 16384 an exact multiple of 256
+// blocks (one per CU).  Output layout of the 32x32 MFMA: lane l holds column
+// l % 32 of rows 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
+template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_mfma_arow(
+    const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W, QW qw,
+    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
+    int64_t ldy, int M, int N, int K, int tiles_n) {
+  constexpr int NT = 256, BM = 256, BK = 64;
+  constexpr int TM = 2, TN = BN / 32;  // 32x32 blocks per wave
+  constexpr int KS = BK / 16;          // k16 substeps per stage
+  constexpr int B_LD = BN * 8 / NT;
+  constexpr int BNO = GEGLU ? BN / 2 : BN;
+  static_assert(B_LD * NT == BN * 8 && BN % 32 == 0, "BN must be a multiple of 32");
+  static_assert(!GEGLU || (TN % 2 == 0), "GEGLU needs an even number of column blocks");
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* Bs = smem;  // [2][BN*64]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, lg = lane >> 5;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int m0 = (tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BNO;
+  const int arow = m0 + wave * 64 + l32;  // + 32 * rb
+
+  auto w_row = [&](int r) -> int {
+    if constexpr (GEGLU) return r < BN / 2 ? n0 + r : N + n0 + (r - BN / 2);
+    else return n0 + r;
+  };
+  auto w_valid = [&](int r) -> bool {
+    if constexpr (GEGLU) return n0 + (r < BN / 2 ? r : r - BN / 2) < N;
+    else return n0 + r < N;
+  };
+
+  // Loads are branch-free: addresses are clamped into the operand.  Rows past
+  // M (A) or N (W) only feed outputs that are never stored, so they need no
+  // zeroing; a K tail (K % 64 != 0, KTAIL) is zeroed.
+  auto load_a = [&](int k0, uint4v (&a)[TM][KS]) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          uint16_t lo = from_f<BF16>(to_f<BF16>(vv[e] & 0xffff) + to_f<BF16>(rr[e] & 0xffff));
-          uint16_t hi = from_f<BF16>(to_f<BF16>(vv[e] >> 16) + to_f<BF16>(rr[e] >> 16));
-          vv[e] = (uint32_t)lo | ((uint32_t)hi << 16);
-        }
-        v = uint4v{vv[0], vv[1], vv[2], vv[3]};
+    for (int rb = 0; rb < TM; rb++)
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        const int row = arow + rb * 32, k = k0 + s * 16 + lg * 8;
+        const uint4v v = *(const uint4v*)(X + (int64_t)(row < M ? row : M - 1) * ldx + (KTAIL && k >= K ? 0 : k));
+        a[rb][s] = (KTAIL && k >= K) ? uint4v{0, 0, 0, 0} : v;
       }
-      *(uint4v*)(Y + (int64_t)gm * ldy + gn) = v;
-    } else {
-      uint16_t vs[8];
-      __builtin_memcpy(vs, &v, 16);
-      for (int e = 0; e < 8 && gn + e < N; e++) {
-        uint16_t o = vs[e];
-        if (R != nullptr) o = from_f<BF16>(to_f<BF16>(o) + to_f<BF16>(R[(int64_t)gm * ldr + gn + e]));
-        Y[(int64_t)gm * ldy + gn + e] = o;
+  };
+
+  struct BRegs {
+    uint4v v[B_LD];
+    uint32_t s[QB ? B_LD : 1], z[QB ? B_LD : 1];
+    float sf[QB && SF32 ? B_LD : 1], zf[QB && SF32 ? B_LD : 1];
+  };
+  auto load_b = [&](int k0, BRegs& br) {
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      int k = k0 + c * 8;
+      bool ok = w_valid(r) && k < K;
+      if constexpr (QB == 0) {
+        const int wr = w_valid(r) ? w_row(r) : 0;
+        const uint4v v = *(const uint4v*)(W + (int64_t)wr * K + (KTAIL && k >= K ? 0 : k));
+        br.v[i] = (KTAIL && k >= K) ? uint4v{0, 0, 0, 0} : v;
+      } else {
+        br.v[i] = uint4v{0, 0, 0, 0};
+        br.s[i] = br.z[i] = 0;
+        if constexpr (SF32) br.sf[i] = br.zf[i] = 0.f;
+        if (ok) {
+          int64_t row = w_row(r);
+          if constexpr (QB == 8) {
+            uint2v w = *(const uint2v*)(qw.q + row * K + k);
+            br.v[i].x = w.x;
+            br.v[i].y = w.y;
+          } else {
+            br.v[i].x = *(const uint32_t*)(qw.q + row * (K / 2) + k / 2);
+          }
+          int64_t gi = row * qw.G + k / qw.group;
+          if constexpr (SF32) {
+            br.sf[i] = ((const float*)qw.scales)[gi];
+            if constexpr (AFF) br.zf[i] = ((const float*)qw.zeros)[gi];
+          } else {
+            br.s[i] = ((const uint16_t*)qw.scales)[gi];
+            if constexpr (AFF) br.z[i] = ((const uint16_t*)qw.zeros)[gi];
+          }
+        }
+      }
+    }
+  };
+  auto store_b = [&](int buf, const BRegs& br) {
+    uint16_t* b = Bs + buf * BN * BK;
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      if constexpr (QB == 0) {
+        *(uint4v*)(b + swz(r, c)) = br.v[i];
+      } else {
+        float sf = 0.f, zf = 0.f;
+        if constexpr (SF32) {
+          sf = br.sf[i];
+          zf = br.zf[i];
+        }
+        *(uint4v*)(b + swz(r, c)) = dequant8<QB, AFF, SF32, BF16>(br.v[i].x, br.v[i].y, br.s[i], br.z[i], sf, zf);
+      }
+    }
+  };
+  // column block j of the tile -> W tile row (GEGLU: value blocks, then gate blocks)
+  auto bcol = [&](int j) -> int {
+    if constexpr (GEGLU) return j < TN / 2 ? j * 32 : BN / 2 + (j - TN / 2) * 32;
+    else return j * 32;
+  };
+
+  float16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  const int KT = (K + BK - 1) / BK;
+  uint4v A0[TM][KS], A1[TM][KS], A2[TM][KS];
+  BRegs B0, B1;
+  // step kt: MFMAs on `ac` and LDS buffer kt&1; loads stage kt+2 into
+  // (al, bl); stages the W tile of kt+1 (held in bs) into the other buffer.
+  auto step = [&](int kt, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl, BRegs& bs) {
+    const int k2 = (kt + 2 < KT ? kt + 2 : KT - 1) * BK;
+    load_a(k2, al);
+    load_b(k2, bl);
+    const uint16_t* b = Bs + (kt & 1) * BN * BK;
+    uint4v bf[KS][TN];
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) bf[s][j] = *(const uint4v*)(b + swz(bcol(j) + l32, 2 * s + lg));
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) acc[i][j] = mfma32<BF16>(ac[i][s], bf[s][j], acc[i][j]);
+    // schedule: global loads, substep-0 reads, then (1 read of the next
+    // substep, 2 MFMAs) pairs, the last substep's MFMAs, the W staging
+    __builtin_amdgcn_sched_group_barrier(0x020, TM * KS + B_LD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
+#pragma unroll
+    for (int s = 0; s < KS - 1; s++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
+      }
+    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+    store_b((kt + 1) & 1, bs);
+    __builtin_amdgcn_sched_group_barrier(0x200, B_LD, 0);
+    __syncthreads();
+  };
+
+  load_a(0, A0);
+  load_b(0, B0);
+  store_b(0, B0);
+  const int k1s = (KT > 1 ? 1 : 0) * BK;
+  load_a(k1s, A1);
+  load_b(k1s, B1);
+  __syncthreads();
+  for (int kt = 0; kt < KT; kt += 6) {
+    step(kt, A0, A2, B0, B1);
+    if (kt + 1 < KT) step(kt + 1, A1, A0, B1, B0);
+    if (kt + 2 < KT) step(kt + 2, A2, A1, B0, B1);
+    if (kt + 3 < KT) step(kt + 3, A0, A2, B1, B0);
+    if (kt + 4 < KT) step(kt + 4, A1, A0, B0, B1);
+    if (kt + 5 < KT) step(kt + 5, A2, A1, B1, B0);
+  }
+
+  // ---- epilogue: bias, one rounding, GeGLU, stage in LDS as [BM][BNO]
+  uint16_t* Cs = smem;
+  constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+#pragma unroll
+    for (int j = 0; j < OUT_TN; j++) {
+      const int ocol = j * 32 + l32;
+      const int gcol = n0 + ocol;
+      float bv = 0.f, bg = 0.f;
+      if (bias != nullptr && gcol < N) {
+        bv = to_f<BF16>(bias[gcol]);
+        if constexpr (GEGLU) bg = to_f<BF16>(bias[N + gcol]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int orow = wave * 64 + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+        float v = to_f<BF16>(from_f<BF16>(acc[i][j][r] + bv));
+        if constexpr (GEGLU) {
+          float g = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][r] + bg));
+          v = gelu_erf(v) * g;
+        }
+        Cs[orow * BNO + ocol] = from_f<BF16>(v);
       }
     }
   }
+  __syncthreads();
+  write_tile<BF16, BM, BNO, NT>(Cs, m0, n0, M, N, R, ldr, Y, ldy);
 }
 
 // ------------------------------------------------------------------ SIMT kernel (f32 path, fallback)
@@ -433,13 +666,32 @@ static void launch_mfma(hipStream_t st, const uint16_t* x, int64_t ldx, const ui
   kern<<<tiles_m * tiles_n, WM * WN * 64, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n);
 }
 
+template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
+static void launch_arow(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw, const uint16_t* bias,
+                        const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K) {
+  constexpr int BNO = GEGLU ? BN / 2 : BN;
+  int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO;
+  size_t stage = (size_t)2 * BN * 64 * sizeof(uint16_t);
+  size_t ctile = (size_t)256 * BNO * sizeof(uint16_t);
+  size_t lds = stage > ctile ? stage : ctile;
+  auto kern = gemm_mfma_arow<BN, BF16, GEGLU, QB, AFF, SF32, KTAIL>;
+  static bool attr = false;
+  if (!attr) {
+    HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = true;
+  }
+  kern<<<tiles_m * tiles_n, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n);
+}
+
 template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
 static void mfma_dispatch(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
                           const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
                           int K) {
-  // 256x128 tiles (4 waves of 128x64) for large M, 128x128 otherwise
-  if ((int64_t)M >= 4096)
-    launch_mfma<256, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  // large M: 256 x 192 tiles with register-resident A rows; otherwise 128 x 128
+  if ((int64_t)M >= 4096 && K % 64 == 0)
+    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, false>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  else if ((int64_t)M >= 4096)
+    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   else
     launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
 }

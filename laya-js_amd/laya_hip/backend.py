@@ -104,6 +104,9 @@ class _Storage:
     def release(self):
         self.refs -= 1
         if self.refs == 0 and self.ptr:
+            for p in self.cache.values():  # device summaries derived from this storage
+                self.owner._free(p)
+            self.cache.clear()
             self.owner._free(self.ptr)
             self.ptr = 0
 
@@ -218,7 +221,8 @@ class HipBackend:
 
     # ---------------------------------------------------------------- plumbing
     # kernel-launching entry points (timed per op key while profiling)
-    _LAUNCHES = frozenset(("hb_linear", "hb_qlinear", "hb_qgather", "hb_layernorm", "hb_rope", "hb_sdpa", "hb_geglu",
+    _LAUNCHES = frozenset(("hb_linear", "hb_qlinear", "hb_qgather", "hb_layernorm", "hb_rope", "hb_sdpa",
+                           "hb_sdpa_mask_info", "hb_geglu",
                            "hb_unary", "hb_binary", "hb_where", "hb_gather", "hb_reduce", "hb_scan", "hb_meanpool"))
 
     def _call(self, op: str, name: str, *args):
@@ -1023,6 +1027,7 @@ class HipBackend:
             _broadcast_shape(mc.shape, full)
             ms = self._bstrides(mc, full)
             mp = self._ptr(mc)
+        info = self._mask_info(mc, ms, B, Lq, Lk) if mc is not None else 0
         # output physically [B, Lq, H, D], returned as a [B, H, Lq, D] view
         st = self._malloc(B * Lq * H * D * DT[dt][1])
         ostr = (Lq * H * D, D, H * D, 1)
@@ -1032,11 +1037,28 @@ class HipBackend:
             if rq or rk:
                 self.stats["sdpa_fused_rope"] += 1
             self._call("sdpa", "hb_sdpa", self.ctx, DT[dt][0], qp, F.i64s(qs), kp, F.i64s(ks), vp, F.i64s(vs), mp,
-                       F.i64s(ms) if ms is not None else None, st.ptr, F.i64s(ostr), B, H, Lq, Lk, D, float(scale),
-                       rq, rk)
+                       F.i64s(ms) if ms is not None else None, info, st.ptr, F.i64s(ostr), B, H, Lq, Lk, D,
+                       float(scale), rq, rk)
         if mc is not None and mc is not mask:
             self.dispose(mc)
         return out
+
+    def _mask_info(self, mc: HipTensor, ms, B: int, Lq: int, Lk: int) -> int:
+        """Device summary of a bool mask (per-tile: no / all / some keys
+        visible), built once per mask view and cached on its storage, so the
+        14 sliding-window layers of an encode share one pass over the mask."""
+        if ms[1] != 0 or not (B and Lq and Lk):
+            return 0
+        key = ("sdpa_tiles", mc._off, tuple(ms), B, Lq, Lk)
+        cache = mc._st.cache
+        if key not in cache:
+            n = F.C.c_size_t(0)
+            self._call("sdpa", "hb_sdpa_mask_info_bytes", B, Lq, Lk, F.C.byref(n))
+            p = F.U(0)
+            self._call("sdpa", "hb_alloc", self.ctx, max(1, n.value), F.C.byref(p))
+            self._call("sdpa", "hb_sdpa_mask_info", self.ctx, self._ptr(mc), F.i64s(ms), B, Lq, Lk, p.value)
+            cache[key] = p.value
+        return cache[key]
 
     # ---------------------------------------------------------------- optional fused ops
     def geglu(self, x: HipTensor) -> HipTensor:

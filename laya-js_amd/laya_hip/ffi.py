@@ -56,7 +56,9 @@ SYMBOLS: dict[str, tuple] = {
     "hb_qgather": (I, [U, U, U, U, I64, I64, I, I, I, U, I64, I, U]),
     "hb_layernorm": (I, [U, I, U, I64, I, U, U, I, U, I64, I64, F]),
     "hb_rope": (I, [U, I, U, PI64, I, U, I64, I64, I64, I64, D]),
-    "hb_sdpa": (I, [U, I, U, PI64, U, PI64, U, PI64, U, PI64, U, PI64, I64, I64, I64, I64, I64, F, D, D]),
+    "hb_sdpa": (I, [U, I, U, PI64, U, PI64, U, PI64, U, PI64, U, U, PI64, I64, I64, I64, I64, I64, F, D, D]),
+    "hb_sdpa_mask_info_bytes": (I, [I64, I64, I64, C.POINTER(C.c_size_t)]),
+    "hb_sdpa_mask_info": (I, [U, U, PI64, I64, I64, I64, U]),
     "hb_geglu": (I, [U, I, U, I64, I, U, I64, I64]),
     "hb_unary": (I, [U, I, I, U, PI64, I, U, PI64, PI64, I, D]),
     "hb_binary": (I, [U, I, I, U, PI64, I, U, PI64, I, U, PI64, I]),
