@@ -8,16 +8,22 @@ contract on libhipbackend.so, driven by the unchanged encoder code.  Inputs
 are random-init fp16 ~N(0, 0.02) with LayerNorm gamma = 1; ids uniform in
 [0, 50368).
 
-Prints ONE JSON line on stdout.  Also reported:
-- roofline of the dominant kernel family (the linear-layer MFMA GEMMs:
-  4 launches per layer), from HIP events around each launch in a profiled
-  pass after the timed region;
+Prints ONE JSON line on stdout.  `value` comes from a clean timed region
+(HIP events around K steps, nothing else instrumented).  Also reported:
+- roofline of the dominant kernel, the large-M linear GEMM
+  (gemm_mfma_arow, f16, plain epilogue: Wqkv, attn Wo and mlp Wo of every
+  layer): a second timed region of K steps with HIP events around each
+  linear launch on the backend's stream gives its average launch time;
+  achieved = algorithmic 2*M*N*K per launch / that time.  `traffic` is the
+  HBM bytes per launch read from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+  summary committed in profiles/ (null when absent);
 - cpu_baseline: the CPU oracle (a C restatement of the reference's CPU
   backend, OpenMP over the host cores) on a bounded sample of the same
   workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
   python bench.py --mode gemm    # isolated config-1/2 GEMM sweep (stderr table + JSON lines)
+  python bench.py --mode copy    # the library's contiguous copy kernel (HBM counter calibration)
 """
 from __future__ import annotations
 
@@ -72,6 +78,33 @@ def linear_flops_per_forward(cfg: dict, M: int) -> float:
     return float(per_layer * L)
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_mfma_arow_config3_hbm_counters.md")
+
+
+def _is_dominant(key: str) -> bool:
+    """linear[M=..,N=..,K=..] launches served by the large-M f16 kernel with a
+    plain (non-GeGLU) epilogue."""
+    return key.startswith("linear[") and "geglu" not in key and int(key.split("M=")[1].split(",")[0]) >= 4096
+
+
+def _key_flops(key: str) -> float:
+    f = dict(kv.split("=") for kv in key[key.index("[") + 1:key.index("]")].split(",") if "=" in kv)
+    return 2.0 * int(f["M"]) * int(f["N"]) * int(f["K"])
+
+
+def _profiled_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 counter summary (line `hbm_bytes_per_launch: <n>`), or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.strip().startswith("hbm_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1].strip().split()[0])
+    except OSError:
+        pass
+    return None
+
+
 def run_encode(args) -> dict:
     from laya_hip.backend import HipBackend
     from laya_hip.host import HostTensor
@@ -102,38 +135,46 @@ def run_encode(args) -> dict:
     for _ in range(args.warmup):
         be.dispose(step())
     be.flush()
-    ev0, ev1 = be.event(), be.event()
-    be.flush()
-    wall0 = time.perf_counter()
-    be.record(ev0)
-    for _ in range(args.steps):
-        be.dispose(step())
-    be.record(ev1)
-    be.flush()
-    wall = time.perf_counter() - wall0
-    gpu_ms = be.elapsed_ms(ev0, ev1)
+
+    def timed(n):
+        ev0, ev1 = be.event(), be.event()
+        be.flush()
+        wall0 = time.perf_counter()
+        be.record(ev0)
+        for _ in range(n):
+            be.dispose(step())
+        be.record(ev1)
+        be.flush()
+        return be.elapsed_ms(ev0, ev1), time.perf_counter() - wall0
+
+    gpu_ms, wall = timed(args.steps)
     ms_per_step = gpu_ms / args.steps
     tokens = B * T
     valid_tokens = int(valid.sum())
     log(f"timed {args.steps} steps: {gpu_ms:.2f} ms on the stream ({wall * 1e3:.2f} ms wall) "
         f"-> {ms_per_step:.3f} ms/step")
 
-    # profiled pass (after the timed region): per-launch GPU time by op key
-    be.startProfiling()
-    for _ in range(args.profile_steps):
-        be.dispose(step())
+    # second timed region: HIP events around every linear launch (on the
+    # backend's stream) -> per-launch GPU time by shape
+    be.startProfiling(only={"hb_linear"})
+    gpu_ms2, _ = timed(args.steps)
     prof = be.stopProfiling()
-    lin_ms = sum(t for k, (n, t) in prof.items() if k.startswith(("linear[", "quantizedLinear[")))
-    lin_launches = sum(n for k, (n, t) in prof.items() if k.startswith(("linear[", "quantizedLinear[")))
-    lin_ms /= args.profile_steps
-    lin_launches //= args.profile_steps
-    prof_total = sum(t for (n, t) in prof.values()) / args.profile_steps
+    log(f"instrumented region: {gpu_ms2 / args.steps:.3f} ms/step")
+    dom = {k: v for k, v in prof.items() if _is_dominant(k)}
+    dom_n = sum(n for n, t in dom.values())
+    dom_ms = sum(t for n, t in dom.values())
+    dom_flops = sum(n * _key_flops(k) for k, (n, t) in dom.items())
+    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    lin_ms = sum(t for n, t in prof.values()) / args.steps
+    lin_launches = sum(n for n, t in prof.values()) // args.steps
     lin_flops = linear_flops_per_forward(BASE, tokens)
-    achieved = lin_flops / (lin_ms * 1e-3) / 1e12
-    log("profiled pass (per forward):")
+    log("linear launches per forward:")
     for k, (n, t) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
-        log(f"  {k:58s} launches {n // args.profile_steps:4d}  {t / args.profile_steps:8.3f} ms")
-    log(f"  sum of kernel times {prof_total:.3f} ms vs timed step {ms_per_step:.3f} ms")
+        log(f"  {k:44s} launches {n // args.steps:4d}  avg {t / n * 1e3:8.1f} us  "
+            f"{_key_flops(k) / (t / n * 1e-3) / 1e12:7.1f} TFLOP/s")
+    log(f"dominant kernel: {dom_n // args.steps} launches/forward, avg {dom_ms / dom_n * 1e3:.1f} us, "
+        f"{achieved:.1f} TFLOP/s")
+    traffic = _profiled_traffic()
 
     out = be.read(step())
     finite = bool(np.isfinite(out.data.astype(np.float32)).all())
@@ -162,13 +203,17 @@ def run_encode(args) -> dict:
             "valid_tokens_per_s": valid_tokens / (ms_per_step * 1e-3),
             "linear_tflop_per_step": lin_flops / 1e12,
             "linear_ms_per_step": lin_ms, "linear_launches_per_step": lin_launches,
-            "linear_mfma_util_pct": 100.0 * achieved / PEAK_F16_TFLOPS,
+            "linear_tflops": lin_flops / (lin_ms * 1e-3) / 1e12,
+            "linear_mfma_util_pct": 100.0 * lin_flops / (lin_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS,
             "output_finite": finite, "device": info.get("name"),
         },
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_F16_TFLOPS, "traffic": None,
-                     "kernel": "gemm_mfma (the 4 linear layers of every encoder layer; algorithmic 2*M*N*K "
-                               f"= {lin_flops / 1e12:.3f} TFLOP per forward over {lin_launches} launches)"},
+                     "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
+                     "kernel": "gemm_mfma_arow (f16, plain epilogue): Wqkv 16384x2304x768, attn Wo "
+                               "16384x768x768 and mlp Wo 16384x768x1152 of every layer; algorithmic 2*M*N*K = "
+                               f"{dom_flops / dom_n / 1e9:.2f} GFLOP per launch on average over "
+                               f"{dom_n // args.steps} launches per forward; avg launch {dom_ms / dom_n * 1e3:.1f} us",
+                     "avg_launch_us": dom_ms / dom_n * 1e3},
     }
     return res
 
@@ -251,13 +296,42 @@ def run_gemm_sweep(args) -> None:
     be.destroy()
 
 
+def run_copy(args) -> None:
+    """The library's contiguous copy kernel (copy_bytes_kernel via hb_unary
+    COPY) over a buffer of known size: reference for the HBM counters."""
+    from laya_hip import ffi as F
+    from laya_hip.backend import HipBackend
+    be = HipBackend(0)
+    nbytes = args.copy_mib << 20
+    src, dst = be._malloc(nbytes), be._malloc(nbytes)
+    n = nbytes // 2
+    shape, xs = F.i64s([n]), F.i64s([1])
+
+    def launch():
+        be.n.call("copy", "hb_unary", be.ctx, F.HB_UN_COPY, F.HB_F16, src.ptr, xs, F.HB_F16, dst.ptr, None, shape,
+                  1, 0.0)
+    for _ in range(3):
+        launch()
+    a, b = be.event(), be.event()
+    be.flush()
+    be.record(a)
+    for _ in range(args.steps):
+        launch()
+    be.record(b)
+    ms = be.elapsed_ms(a, b) / args.steps
+    print(json.dumps({"mode": "copy", "kernel": "copy_bytes_kernel", "bytes_read_per_launch": nbytes,
+                      "bytes_written_per_launch": nbytes, "us_per_launch": ms * 1e3,
+                      "GB_per_s": 2 * nbytes / (ms * 1e-3) / 1e9}), flush=True)
+    be.destroy()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--profile-steps", type=int, default=2)
-    ap.add_argument("--mode", choices=["encode", "gemm"], default="encode")
+    ap.add_argument("--mode", choices=["encode", "gemm", "copy"], default="encode")
+    ap.add_argument("--copy-mib", type=int, default=512, help="buffer size for --mode copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-sample", type=int, default=8, help="sequences in the CPU-baseline sample")
     args = ap.parse_args()
@@ -268,6 +342,9 @@ def main():
         sys.exit(2)
     if args.mode == "gemm":
         run_gemm_sweep(args)
+        return
+    if args.mode == "copy":
+        run_copy(args)
         return
     res = run_encode(args)
     if not args.no_cpu:

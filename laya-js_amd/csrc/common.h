@@ -29,6 +29,7 @@ void check_launch(const char* what);
 struct Context;
 hipStream_t stream_of(uintptr_t ctx);
 int device_of(uintptr_t ctx);
+int cu_count(uintptr_t ctx);
 // scratch memory from the context's stream-ordered pool (freed with pool_free)
 void* pool_alloc(uintptr_t ctx, size_t bytes);
 void pool_free(uintptr_t ctx, void* p);
@@ -140,6 +141,23 @@ __device__ __forceinline__ float pin_f32(float x) {
 }
 
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+// GELU for 16-bit outputs (the fused GeGLU epilogue of the GEMMs): erf by
+// Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26,
+// erf(z) = 1 - t(a1 + t(a2 + t(a3 + t(a4 + t a5)))) exp(-z^2), t = 1/(1 + p z),
+// |error| <= 1.5e-7 for z >= 0.  For x < 0, 1 + erf = t(...)exp(-z^2) is used
+// directly, so the left tail keeps its relative accuracy.  The result is well
+// inside half a unit of f16 / bf16 precision of gelu.
+__device__ __forceinline__ float gelu_fast(float x) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  float p = fmaf(t, 1.061405429f, -1.453152027f);
+  p = fmaf(t, p, 1.421413741f);
+  p = fmaf(t, p, -0.284496736f);
+  p = fmaf(t, p, 0.254829592f);
+  const float pe = p * t * __expf(-z * z);  // 1 - erf(z)
+  return 0.5f * x * (x >= 0.f ? 2.0f - pe : pe);
+}
 
 // ------------------------------------------------------------------ wave reductions (wave64)
 

@@ -2,21 +2,25 @@
 // 16-bit weights and for laya's quantized weight format (q8 / q4 with
 // per-group scales and zeros).
 //
-// The hot path is gemm_mfma: fp16 / bf16 operands on gfx950's
-// v_mfma_f32_16x16x32_{f16,bf16}, both operands K-contiguous ("NT"), A and B
-// tiles double-buffered in LDS (64-wide K stages, 16-byte chunks XOR-swizzled
-// by row so the fragment reads of 16 consecutive rows spread over the banks),
-// and an epilogue that adds bias, rounds once to the storage type, applies
-// GeGLU on (value, gate) column pairs held by the same lane, stages the tile in
-// LDS and writes it with 16-byte coalesced stores, adding the residual there.
-// For quantized weights the B loader fetches the packed codes (8 or 4 bytes
-// per 8 weights) and the group's scale / zero, dequantizes them in registers
-// to fl16(q*s + z) -- one correctly rounded f16 fma, the value host
+// Two MFMA kernels, both on gfx950's v_mfma_f32_32x32x16_{f16,bf16} with the
+// same operand order (W rows as the A operand, X rows as the B operand) and
+// the same sequence of k16 steps, so a row's output bits do not depend on M:
+// - gemm_mfma_arow (M >= 4096): persistent, 256 x 192 tiles, X rows in
+//   registers, W tiles double-buffered in LDS, epilogue from registers;
+// - gemm_mfma (smaller M): 128 x 128 tiles, A and B double-buffered in LDS,
+//   epilogue staged in LDS and written with 16-byte stores.
+// Both take 64-wide K stages of 16-byte chunks XOR-swizzled by row so the
+// fragment reads of consecutive rows spread over the LDS banks.  The
+// epilogue adds the bias, rounds once to the storage type, applies GeGLU on
+// (value, gate) column pairs held by the same lane, and adds the residual
+// (y = round(round(x.w^T + b) + r), the linear-then-add order).  For
+// quantized weights the W loader fetches the packed codes (8 or 4 bytes per
+// 8 weights) and the group's scale / zero, dequantizes them in registers to
+// fl16(q*s + z) -- one correctly rounded f16 fma, the value host
 // dequantization would upload -- and stages f16 into LDS for the same MFMA.
 // Blocks walk the tile grid in an XCD-aware order: the hardware deals block b
-// to XCD b % 8, so block b is given the tile that keeps each XCD on a
-// contiguous run of row panels (their A rows and the whole W stay in that
-// XCD's L2).
+// to XCD b % 8, so each XCD is given a contiguous run of row panels (their A
+// rows and the whole W stay in that XCD's L2).
 //
 // gemm_simt is the f32 path (and the fallback for shapes the MFMA kernel's
 // 16-byte loads cannot take: K or row strides not a multiple of 8).
@@ -28,13 +32,14 @@ namespace hb {
 
 // ------------------------------------------------------------------ helpers
 
+
 template <bool BF16>
-__device__ __forceinline__ float4v mfma16(const uint4v& a, const uint4v& b, float4v c) {
+__device__ __forceinline__ float16v mfma32(const uint4v& a, const uint4v& b, float16v c) {
   if constexpr (BF16) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                    0, 0);
   } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
                                                   0, 0);
   }
 }
@@ -166,7 +171,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
   constexpr int NT = WM * WN * 64;
   constexpr int BK = 64;
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
-  constexpr int TM = WTM / 16, TN = WTN / 16;  // 16x16 blocks per wave
+  constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 blocks per wave
   constexpr int A_LD = BM * 8 / NT, B_LD = BN * 8 / NT;
   constexpr int BNO = GEGLU ? BN / 2 : BN;  // output columns per tile
   static_assert(A_LD * NT == BM * 8 && B_LD * NT == BN * 8, "tile/threads mismatch");
@@ -263,17 +268,20 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
   auto bcol = [&](int tn) -> int {
     if constexpr (GEGLU) {
       constexpr int H = TN / 2;
-      return tn < H ? wn * (WTN / 2) + tn * 16 : BN / 2 + wn * (WTN / 2) + (tn - H) * 16;
+      return tn < H ? wn * (WTN / 2) + tn * 32 : BN / 2 + wn * (WTN / 2) + (tn - H) * 32;
     } else {
-      return wn * WTN + tn * 16;
+      return wn * WTN + tn * 32;
     }
   };
 
-  float4v acc[TM][TN];
+  float16v acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+  const int l32 = lane & 31, lg = lane >> 5;
 
   const int KT = (K + BK - 1) / BK;
   load_regs(0);
@@ -284,47 +292,57 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
     if (kt + 1 < KT) load_regs((kt + 1) * BK);
     const uint16_t* a = As + buf * BM * BK;
     const uint16_t* b = Bs + buf * BN * BK;
+    // k16 substeps in increasing k; W rows as the A operand and X rows as
+    // the B operand, the order the large-M kernel uses, so both kernels
+    // produce the same bits for a row whatever M is
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
-      const int c = s * 4 + (lane >> 4);
+    for (int s = 0; s < 4; s++) {
+      const int c = 2 * s + lg;
       uint4v af[TM], bf[TN];
 #pragma unroll
-      for (int i = 0; i < TM; i++) af[i] = *(const uint4v*)(a + swz(wm * WTM + i * 16 + (lane & 15), c));
+      for (int i = 0; i < TM; i++) af[i] = *(const uint4v*)(a + swz(wm * WTM + i * 32 + l32, c));
 #pragma unroll
-      for (int j = 0; j < TN; j++) bf[j] = *(const uint4v*)(b + swz(bcol(j) + (lane & 15), c));
+      for (int j = 0; j < TN; j++) bf[j] = *(const uint4v*)(b + swz(bcol(j) + l32, c));
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = mfma16<BF16>(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < TN; j++) acc[i][j] = mfma32<BF16>(bf[j], af[i], acc[i][j]);
     }
     if (kt + 1 < KT) store_lds(buf ^ 1);
     __syncthreads();
   }
 
-  // ---- epilogue: bias, one rounding, GeGLU, stage in LDS as [BM][BNO]
+  // ---- epilogue: bias, one rounding, GeGLU, stage in LDS as [BM][BNO];
+  // lane l holds row l % 32 and columns 8*(r/4) + 4*(l/32) + {0..3}
   uint16_t* Cs = smem;
   constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
   constexpr int WTNO = GEGLU ? WTN / 2 : WTN;
 #pragma unroll
   for (int i = 0; i < TM; i++) {
+    const int orow = wm * WTM + i * 32 + l32;
 #pragma unroll
     for (int j = 0; j < OUT_TN; j++) {
-      const int ocol = wn * WTNO + j * 16 + (lane & 15);  // tile output column
-      const int gcol = n0 + ocol;
-      float bv = 0.f, bg = 0.f;
-      if (bias != nullptr && gcol < N) {
-        bv = to_f<BF16>(bias[gcol]);
-        if constexpr (GEGLU) bg = to_f<BF16>(bias[N + gcol]);
-      }
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int orow = wm * WTM + i * 16 + (lane >> 4) * 4 + r;
-        float v = to_f<BF16>(from_f<BF16>(acc[i][j][r] + bv));
-        if constexpr (GEGLU) {
-          float g = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][r] + bg));
-          v = gelu_erf(v) * g;
+      for (int g = 0; g < 4; g++) {
+        const int ocol = wn * WTNO + j * 32 + 8 * g + 4 * lg;  // tile output column of element 0
+        uint16_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int gcol = n0 + ocol + e;
+          float bv = 0.f, bg = 0.f;
+          if (bias != nullptr && gcol < N) {
+            bv = to_f<BF16>(bias[gcol]);
+            if constexpr (GEGLU) bg = to_f<BF16>(bias[N + gcol]);
+          }
+          float v = to_f<BF16>(from_f<BF16>(acc[i][j][4 * g + e] + bv));
+          if constexpr (GEGLU) {
+            const float gt = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][4 * g + e] + bg));
+            v = gelu_fast(v) * gt;
+          }
+          o[e] = from_f<BF16>(v);
         }
-        Cs[orow * BNO + ocol] = from_f<BF16>(v);
+        *(uint2v*)(Cs + orow * BNO + ocol) =
+            uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
       }
     }
   }
@@ -335,33 +353,31 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
 
 // ------------------------------------------------------------------ large-M MFMA kernel
 
-template <bool BF16>
-__device__ __forceinline__ float16v mfma32(const uint4v& a, const uint4v& b, float16v c) {
-  if constexpr (BF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
-                                                   0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
-                                                  0, 0);
-  }
-}
 
-// 256 x BN output tile, four waves stacked along M: each wave owns 64 rows
-// and every column of the tile as 2 x (BN/32) blocks of v_mfma_f32_32x32x16
-// (on gfx950 the 32x32 MFMA runs at twice the rate of the 16x16x32 one, and
-// reaches it from a single wave per SIMD).  A wave's A rows are private, so
-// they go from global memory straight into MFMA A-operand registers; only
-// the weight tile is shared, through double-buffered LDS.  Loads run two K
-// stages ahead of the MFMAs (three A and two W register sets rotating by
-// name), so global latency hides behind two stages of MFMA work.  BN = 192
-// makes every ModernBERT-base linear at M = 16384 an exact multiple of 256
-// blocks (one per CU).  Output layout of the 32x32 MFMA: lane l holds column
-// l % 32 of rows 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
+// Persistent GEMM over 256 x BN output tiles.  Four waves are stacked along
+// M: each wave owns 64 rows and every column of the tile as 2 x (BN/32)
+// blocks of v_mfma_f32_32x32x16 (on gfx950 the 32x32 MFMA runs at twice the
+// rate of the 16x16x32 one, and reaches it from a single wave per SIMD).
+// A wave's A rows are private, so they go from global memory straight into
+// MFMA operand registers; only the weight tile is shared, through
+// double-buffered LDS.
+//
+// One block per CU walks a list of tiles as one continuous stream of
+// 64-wide K stages: loads run two stages ahead (three A and two W register
+// sets rotating by name, issued between the MFMAs) and cross tile
+// boundaries, so the next tile's first stages arrive while the current tile
+// finishes.  Blocks on one XCD (block b runs on XCD b % 8) take consecutive
+// tiles, which share A rows in that XCD's L2.
+//
+// The MFMA computes the transposed product (W rows as the A operand, X rows
+// as the B operand): lane l then holds output row l % 32 and the four
+// consecutive columns 8*(r/4) + 4*(l/32) + {0..3} of each accumulator, so the
+// epilogue writes 8-byte pieces of Y straight from registers.
 template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_mfma_arow(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W, QW qw,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
-    int64_t ldy, int M, int N, int K, int tiles_n) {
+    int64_t ldy, int M, int N, int K, int tiles_n, int tiles) {
   constexpr int NT = 256, BM = 256, BK = 64;
   constexpr int TM = 2, TN = BN / 32;  // 32x32 blocks per wave
   constexpr int KS = BK / 16;          // k16 substeps per stage
@@ -375,24 +391,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lg = lane >> 5;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int m0 = (tile / tiles_n) * BM;
-  const int n0 = (tile % tiles_n) * BNO;
-  const int arow = m0 + wave * 64 + l32;  // + 32 * rb
 
-  auto w_row = [&](int r) -> int {
-    if constexpr (GEGLU) return r < BN / 2 ? n0 + r : N + n0 + (r - BN / 2);
-    else return n0 + r;
-  };
-  auto w_valid = [&](int r) -> bool {
-    if constexpr (GEGLU) return n0 + (r < BN / 2 ? r : r - BN / 2) < N;
-    else return n0 + r < N;
-  };
+  // this block's tiles: c0 + slot + i * nx for i < ntile (gridDim.x % 8 == 0)
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, nx = gridDim.x >> 3;
+  const int c0 = (int)((int64_t)xcd * tiles / 8), c1 = (int)((int64_t)(xcd + 1) * tiles / 8);
+  const int ntile = c1 - c0 > slot ? (c1 - c0 - slot + nx - 1) / nx : 0;
+  if (ntile == 0) return;
+  const int KT = (K + BK - 1) / BK;
+  const int S = ntile * KT;  // stages in this block's stream
+  auto tile_m0 = [&](int i) { return ((c0 + slot + i * nx) / tiles_n) * BM; };
+  auto tile_n0 = [&](int i) { return ((c0 + slot + i * nx) % tiles_n) * BNO; };
 
   // Loads are branch-free: addresses are clamped into the operand.  Rows past
   // M (A) or N (W) only feed outputs that are never stored, so they need no
   // zeroing; a K tail (K % 64 != 0, KTAIL) is zeroed.
-  auto load_a = [&](int k0, uint4v (&a)[TM][KS]) {
+  auto load_a = [&](int m0, int k0, uint4v (&a)[TM][KS]) {
+    const int arow = m0 + wave * 64 + l32;
 #pragma unroll
     for (int rb = 0; rb < TM; rb++)
 #pragma unroll
@@ -408,22 +422,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     uint32_t s[QB ? B_LD : 1], z[QB ? B_LD : 1];
     float sf[QB && SF32 ? B_LD : 1], zf[QB && SF32 ? B_LD : 1];
   };
-  auto load_b = [&](int k0, BRegs& br) {
+  // B tile row r -> W row (GEGLU: first half value rows, second half gate rows)
+  auto load_b = [&](int n0, int k0, BRegs& br) {
 #pragma unroll
     for (int i = 0; i < B_LD; i++) {
-      int q = tid + i * NT, r = q >> 3, c = q & 7;
-      int k = k0 + c * 8;
-      bool ok = w_valid(r) && k < K;
+      const int q = tid + i * NT, r = q >> 3, c = q & 7;
+      const int k = k0 + c * 8;
+      const int nn = GEGLU ? n0 + (r < BN / 2 ? r : r - BN / 2) : n0 + r;
+      const bool rv = nn < N;
+      const int wr = GEGLU && r >= BN / 2 ? N + nn : nn;
       if constexpr (QB == 0) {
-        const int wr = w_valid(r) ? w_row(r) : 0;
-        const uint4v v = *(const uint4v*)(W + (int64_t)wr * K + (KTAIL && k >= K ? 0 : k));
+        const uint4v v = *(const uint4v*)(W + (int64_t)(rv ? wr : 0) * K + (KTAIL && k >= K ? 0 : k));
         br.v[i] = (KTAIL && k >= K) ? uint4v{0, 0, 0, 0} : v;
       } else {
         br.v[i] = uint4v{0, 0, 0, 0};
         br.s[i] = br.z[i] = 0;
         if constexpr (SF32) br.sf[i] = br.zf[i] = 0.f;
-        if (ok) {
-          int64_t row = w_row(r);
+        if (rv && k < K) {
+          const int64_t row = wr;
           if constexpr (QB == 8) {
             uint2v w = *(const uint2v*)(qw.q + row * K + k);
             br.v[i].x = w.x;
@@ -431,7 +447,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           } else {
             br.v[i].x = *(const uint32_t*)(qw.q + row * (K / 2) + k / 2);
           }
-          int64_t gi = row * qw.G + k / qw.group;
+          const int64_t gi = row * qw.G + k / qw.group;
           if constexpr (SF32) {
             br.sf[i] = ((const float*)qw.scales)[gi];
             if constexpr (AFF) br.zf[i] = ((const float*)qw.zeros)[gi];
@@ -474,16 +490,77 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  const int KT = (K + BK - 1) / BK;
+  // ---- epilogue from registers: bias, one rounding, GeGLU (value block j,
+  // gate block j + TN/2 hold the same output columns), residual; leaves the
+  // accumulators zeroed for the next tile
+  auto epilogue = [&](int m0, int n0) {
+    constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
+#pragma unroll
+    for (int j = 0; j < OUT_TN; j++) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int ncol = n0 + j * 32 + 8 * g + 4 * lg;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f}, bg[4] = {0.f, 0.f, 0.f, 0.f};
+        if (bias != nullptr) {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (ncol + e < N) {
+              bv[e] = to_f<BF16>(bias[ncol + e]);
+              if constexpr (GEGLU) bg[e] = to_f<BF16>(bias[N + ncol + e]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const int mrow = m0 + wave * 64 + i * 32 + l32;
+          uint16_t o[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            float v = to_f<BF16>(from_f<BF16>(acc[i][j][4 * g + e] + bv[e]));
+            if constexpr (GEGLU) {
+              const float gt = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][4 * g + e] + bg[e]));
+              v = gelu_fast(v) * gt;
+            }
+            o[e] = from_f<BF16>(v);
+          }
+          if (mrow < M && ncol < N) {
+            uint16_t* yp = Y + (int64_t)mrow * ldy + ncol;
+            const uint16_t* rp = R != nullptr ? R + (int64_t)mrow * ldr + ncol : nullptr;
+            if (ncol + 4 <= N) {
+              if (rp != nullptr) {
+                const uint2v rv = *(const uint2v*)rp;
+                const uint16_t rr[4] = {(uint16_t)(rv.x & 0xffff), (uint16_t)(rv.x >> 16),
+                                        (uint16_t)(rv.y & 0xffff), (uint16_t)(rv.y >> 16)};
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = from_f<BF16>(to_f<BF16>(o[e]) + to_f<BF16>(rr[e]));
+              }
+              *(uint2v*)yp =
+                  uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+            } else {
+              for (int e = 0; e < 4 && ncol + e < N; e++)
+                yp[e] = rp != nullptr ? from_f<BF16>(to_f<BF16>(o[e]) + to_f<BF16>(rp[e])) : o[e];
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+  };
+
   uint4v A0[TM][KS], A1[TM][KS], A2[TM][KS];
   BRegs B0, B1;
-  // step kt: MFMAs on `ac` and LDS buffer kt&1; loads stage kt+2 into
-  // (al, bl); stages the W tile of kt+1 (held in bs) into the other buffer.
-  auto step = [&](int kt, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl, BRegs& bs) {
-    const int k2 = (kt + 2 < KT ? kt + 2 : KT - 1) * BK;
-    load_a(k2, al);
-    load_b(k2, bl);
-    const uint16_t* b = Bs + (kt & 1) * BN * BK;
+  // step g: MFMAs on `ac` and LDS buffer g&1; loads stage g+2 of the stream
+  // into (al, bl); stages the W tile of g+1 (held in bs) into the other buffer.
+  auto step = [&](int g, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl, BRegs& bs) {
+    const int g2 = g + 2 < S ? g + 2 : S - 1;
+    const int i2 = g2 / KT, k2 = (g2 - i2 * KT) * BK;
+    load_a(tile_m0(i2), k2, al);
+    load_b(tile_n0(i2), k2, bl);
+    const uint16_t* b = Bs + (g & 1) * BN * BK;
     uint4v bf[KS][TN];
 #pragma unroll
     for (int s = 0; s < KS; s++)
@@ -494,68 +571,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int i = 0; i < TM; i++) acc[i][j] = mfma32<BF16>(ac[i][s], bf[s][j], acc[i][j]);
-    // schedule: global loads, substep-0 reads, then (1 read of the next
-    // substep, 2 MFMAs) pairs, the last substep's MFMAs, the W staging
-    __builtin_amdgcn_sched_group_barrier(0x020, TM * KS + B_LD, 0);
+        for (int i = 0; i < TM; i++) acc[i][j] = mfma32<BF16>(bf[s][j], ac[i][s], acc[i][j]);
+    // schedule: substep-0 fragment reads, then MFMA pairs, each preceded by
+    // one global load (while any remain) and one fragment read of the next
+    // substep; the W staging for the next stage goes last
+    constexpr int NVMEM = TM * KS + B_LD, NPAIR = KS * TN;
     __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
 #pragma unroll
-    for (int s = 0; s < KS - 1; s++)
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
-      }
-    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
-    store_b((kt + 1) & 1, bs);
+    for (int p = 0; p < NPAIR; p++) {
+      if (p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (p < (KS - 1) * TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
+    }
+    store_b((g + 1) & 1, bs);
     __builtin_amdgcn_sched_group_barrier(0x200, B_LD, 0);
     __syncthreads();
   };
 
-  load_a(0, A0);
-  load_b(0, B0);
-  store_b(0, B0);
-  const int k1s = (KT > 1 ? 1 : 0) * BK;
-  load_a(k1s, A1);
-  load_b(k1s, B1);
-  __syncthreads();
-  for (int kt = 0; kt < KT; kt += 6) {
-    step(kt, A0, A2, B0, B1);
-    if (kt + 1 < KT) step(kt + 1, A1, A0, B1, B0);
-    if (kt + 2 < KT) step(kt + 2, A2, A1, B0, B1);
-    if (kt + 3 < KT) step(kt + 3, A0, A2, B1, B0);
-    if (kt + 4 < KT) step(kt + 4, A1, A0, B0, B1);
-    if (kt + 5 < KT) step(kt + 5, A2, A1, B1, B0);
+  {
+    const int m0 = tile_m0(0), n0 = tile_n0(0);
+    const int g1 = S > 1 ? 1 : 0, i1 = g1 / KT, k1 = (g1 - i1 * KT) * BK;
+    load_a(m0, 0, A0);
+    load_b(n0, 0, B0);
+    store_b(0, B0);
+    load_a(tile_m0(i1), k1, A1);
+    load_b(tile_n0(i1), k1, B1);
+    __syncthreads();
   }
-
-  // ---- epilogue: bias, one rounding, GeGLU, stage in LDS as [BM][BNO]
-  uint16_t* Cs = smem;
-  constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
-#pragma unroll
-  for (int i = 0; i < TM; i++) {
-#pragma unroll
-    for (int j = 0; j < OUT_TN; j++) {
-      const int ocol = j * 32 + l32;
-      const int gcol = n0 + ocol;
-      float bv = 0.f, bg = 0.f;
-      if (bias != nullptr && gcol < N) {
-        bv = to_f<BF16>(bias[gcol]);
-        if constexpr (GEGLU) bg = to_f<BF16>(bias[N + gcol]);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int orow = wave * 64 + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-        float v = to_f<BF16>(from_f<BF16>(acc[i][j][r] + bv));
-        if constexpr (GEGLU) {
-          float g = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][r] + bg));
-          v = gelu_erf(v) * g;
-        }
-        Cs[orow * BNO + ocol] = from_f<BF16>(v);
-      }
+  // The register rotation has period 6, so a block streams several tiles
+  // only when KT % 6 == 0 (the launcher gives every block one tile otherwise).
+  for (int it = 0; it < ntile; it++) {
+    const int g0 = it * KT;
+    for (int kt = 0; kt < KT; kt += 6) {
+      step(g0 + kt, A0, A2, B0, B1);
+      if (kt + 1 < KT) step(g0 + kt + 1, A1, A0, B1, B0);
+      if (kt + 2 < KT) step(g0 + kt + 2, A2, A1, B0, B1);
+      if (kt + 3 < KT) step(g0 + kt + 3, A0, A2, B1, B0);
+      if (kt + 4 < KT) step(g0 + kt + 4, A1, A0, B0, B1);
+      if (kt + 5 < KT) step(g0 + kt + 5, A2, A1, B1, B0);
     }
+    epilogue(tile_m0(it), tile_n0(it));
   }
-  __syncthreads();
-  write_tile<BF16, BM, BNO, NT>(Cs, m0, n0, M, N, R, ldr, Y, ldy);
 }
 
 // ------------------------------------------------------------------ SIMT kernel (f32 path, fallback)
@@ -667,45 +723,49 @@ static void launch_mfma(hipStream_t st, const uint16_t* x, int64_t ldx, const ui
 }
 
 template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
-static void launch_arow(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw, const uint16_t* bias,
-                        const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K) {
+static void launch_arow(hipStream_t st, int cus, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
+                        const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
+                        int K) {
   constexpr int BNO = GEGLU ? BN / 2 : BN;
-  int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO;
-  size_t stage = (size_t)2 * BN * 64 * sizeof(uint16_t);
-  size_t ctile = (size_t)256 * BNO * sizeof(uint16_t);
-  size_t lds = stage > ctile ? stage : ctile;
+  const int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO, tiles = tiles_m * tiles_n;
+  // one persistent block per CU, a multiple of 8 (one per XCD); with
+  // K % 384 != 0 one block per tile
+  const int KT = (K + 63) / 64;
+  int grid = KT % 6 == 0 ? (tiles < cus ? tiles : cus) / 8 * 8 : (tiles + 7) / 8 * 8;
+  HB_REQUIRE(grid >= 8, "hb_linear: large-M GEMM needs at least 8 tiles");
+  const size_t lds = (size_t)2 * BN * 64 * sizeof(uint16_t);
   auto kern = gemm_mfma_arow<BN, BF16, GEGLU, QB, AFF, SF32, KTAIL>;
   static bool attr = false;
   if (!attr) {
     HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr = true;
   }
-  kern<<<tiles_m * tiles_n, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n);
+  kern<<<grid, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n, tiles);
 }
 
 template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
-static void mfma_dispatch(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
+static void mfma_dispatch(hipStream_t st, int cus, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
                           const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
                           int K) {
-  // large M: 256 x 192 tiles with register-resident A rows; otherwise 128 x 128
+  // large M: persistent 256 x 192 tiles with register-resident A rows; otherwise 128 x 128
   if ((int64_t)M >= 4096 && K % 64 == 0)
-    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, false>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, false>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   else if ((int64_t)M >= 4096)
-    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   else
     launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
 }
 
 template <int QB, bool AFF, bool SF32>
-static void mfma_dtype(int dt, bool geglu, hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
-                       const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
-                       int K) {
+static void mfma_dtype(int dt, bool geglu, hipStream_t st, int cus, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                       QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
+                       int N, int K) {
   if (dt == HB_F16) {
-    if (geglu) mfma_dispatch<false, true, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-    else mfma_dispatch<false, false, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    if (geglu) mfma_dispatch<false, true, QB, AFF, SF32>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    else mfma_dispatch<false, false, QB, AFF, SF32>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   } else {
-    if (geglu) mfma_dispatch<true, true, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-    else mfma_dispatch<true, false, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    if (geglu) mfma_dispatch<true, true, QB, AFF, SF32>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    else mfma_dispatch<true, false, QB, AFF, SF32>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   }
 }
 
@@ -741,7 +801,7 @@ extern "C" int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintpt
               (!r || ldr % 8 == 0) && x % 16 == 0 && w % 16 == 0 && y % 16 == 0 && (!r || resid % 16 == 0);
   if (mfma) {
     QW qw{nullptr, nullptr, nullptr, 0, 1};
-    mfma_dtype<0, false, false>(dt, geglu, st, (const uint16_t*)x, ldx, (const uint16_t*)w, qw, (const uint16_t*)b,
+    mfma_dtype<0, false, false>(dt, geglu, st, cu_count(ctx), (const uint16_t*)x, ldx, (const uint16_t*)w, qw, (const uint16_t*)b,
                                 (const uint16_t*)r, ldr, (uint16_t*)y, ldy, (int)M, (int)N, (int)K);
   } else {
     QWs qw{nullptr, nullptr, nullptr, 0, 0, 1, 0, 0};
@@ -784,10 +844,10 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
     const uint16_t* Rp = (const uint16_t*)r;
     uint16_t* Yp = (uint16_t*)y;
     int m = (int)M, n = (int)N, k = (int)K;
-    if (bits == 8 && mode == 0) mfma_dtype<8, false, false>(dt, geglu, st, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
-    else if (bits == 8) mfma_dtype<8, true, false>(dt, geglu, st, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
-    else if (mode == 0) mfma_dtype<4, false, false>(dt, geglu, st, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
-    else mfma_dtype<4, true, false>(dt, geglu, st, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    if (bits == 8 && mode == 0) mfma_dtype<8, false, false>(dt, geglu, st, cu_count(ctx), X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else if (bits == 8) mfma_dtype<8, true, false>(dt, geglu, st, cu_count(ctx), X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else if (mode == 0) mfma_dtype<4, false, false>(dt, geglu, st, cu_count(ctx), X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else mfma_dtype<4, true, false>(dt, geglu, st, cu_count(ctx), X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
   } else {
     QWs q{(const uint8_t*)qw, (const void*)scales, (const void*)zeros, HB_F16, G, group, bits, mode};
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));

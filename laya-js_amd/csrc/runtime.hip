@@ -36,6 +36,7 @@ struct Staging {
 
 struct Context {
   int device = 0;
+  int cus = 0;  // compute units of the device
   hipStream_t stream = nullptr;
   std::map<size_t, std::vector<void*>> free_list;  // size class -> blocks
   std::unordered_map<void*, size_t> live;            // block -> size class
@@ -63,6 +64,7 @@ static Context* C(uintptr_t ctx) {
 
 hipStream_t stream_of(uintptr_t ctx) { return C(ctx)->stream; }
 int device_of(uintptr_t ctx) { return C(ctx)->device; }
+int cu_count(uintptr_t ctx) { return C(ctx)->cus; }
 
 void* pool_alloc(uintptr_t ctx, size_t bytes) {
   Context* c = C(ctx);
@@ -194,6 +196,7 @@ int hb_init(int device, uintptr_t* ctx) {
   HB_REQUIRE(arch.rfind("gfx950", 0) == 0, "hb_init: libhipbackend is built for gfx950 (MI355X); device is " + arch);
   Context* c = new Context();
   c->device = device;
+  c->cus = prop.multiProcessorCount;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete c;

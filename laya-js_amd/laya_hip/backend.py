@@ -215,6 +215,7 @@ class HipBackend:
         self._scopes: list[list[HipTensor]] = []
         self._destroyed = False
         self._profiling = None  # list of (key, start event, end event) while profiling
+        self._prof_only = self._LAUNCHES
         self._event_pool: list[int] = []
         self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "sdpa": 0,
                       "sdpa_fused_rope": 0, "copies": 0}
@@ -227,7 +228,7 @@ class HipBackend:
 
     def _call(self, op: str, name: str, *args):
         prof = self._profiling
-        if prof is not None and name in self._LAUNCHES:
+        if prof is not None and name in self._prof_only:
             a, b = self._take_event(), self._take_event()
             self.n.call(op, "hb_event_record", self.ctx, a)
             self.n.call(op, name, *args)
@@ -247,9 +248,12 @@ class HipBackend:
         self.n.call("profile", "hb_event_create", self.ctx, F.C.byref(ev))
         return ev.value
 
-    def startProfiling(self) -> None:
+    def startProfiling(self, only=None) -> None:
         """Times every kernel launch with HIP events on the stream, like the
-        reference's Runtime.startProfiling (backend-webgpu/src/runtime.ts:420-464)."""
+        reference's Runtime.startProfiling (backend-webgpu/src/runtime.ts:420-464).
+        `only`: a set of entry-point names (e.g. {"hb_linear"}) to time instead
+        of every launch."""
+        self._prof_only = self._LAUNCHES if only is None else frozenset(only) & self._LAUNCHES
         self._profiling = []
 
     def stopProfiling(self) -> dict:

@@ -79,6 +79,26 @@ def test_linear_bias_resid_ragged(b, dtype):
     assert b.stats["linear_fused_resid"] > 0
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_linear_geglu_bias_ragged(b, dtype):
+    """GeGLU epilogue with a bias (value and gate halves of the bias) and
+    ragged output widths, on both the small-M and the large-M kernels."""
+    rng = np.random.default_rng(9)
+    for (M, N2, K) in [(300, 770, 136), (4100, 770, 776), (4096, 2304, 768)]:
+        x = rounded(rng.standard_normal((M, K)), dtype)
+        w = rounded(rng.normal(0, 0.05, (N2, K)), dtype)
+        bias = rounded(rng.standard_normal(N2), dtype)
+        X, Wt, Bt = (b.fromHost(to_host(a, dtype)) for a in (x, w, bias))
+        y = b.geglu(b.linear(X, Wt, Bt))
+        got = read32(b, y)
+        rows = _rows(M, rng)
+        ref = cr.geglu(rounded(cr.linear(x[rows], w, bias), dtype))
+        err = max_rel(got[rows], ref)
+        assert err <= (2e-3 if dtype == "f16" else 8e-3), f"M={M} N={N2} K={K}: {err:.2e}"
+        for t in (X, Wt, Bt, y):
+            b.dispose(t)
+
+
 def test_linear_f32_path(b):
     rng = np.random.default_rng(8)
     x = rng.standard_normal((70, 45)).astype(np.float32)
