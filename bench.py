@@ -176,6 +176,17 @@ def run_encode(args) -> dict:
         f"{achieved:.1f} TFLOP/s")
     traffic = _profiled_traffic()
 
+    # host-to-host rate (ids and mask uploaded, output read back): never `value`
+    be.dispose(step())
+    be.flush()
+    w0 = time.perf_counter()
+    for _ in range(3):
+        inp2 = enc.uploadInputs(ids, valid, B, T)
+        out = be.read(enc.encode(inp2))
+        enc.disposeInputs(inp2)
+    pcie_ms = (time.perf_counter() - w0) / 3 * 1e3
+    log(f"host-to-host (upload ids/mask, encode, read [{B},{T},768] f16 back): {pcie_ms:.2f} ms/step")
+
     out = be.read(step())
     finite = bool(np.isfinite(out.data.astype(np.float32)).all())
     enc.disposeInputs(inp)
@@ -205,7 +216,8 @@ def run_encode(args) -> dict:
             "linear_ms_per_step": lin_ms, "linear_launches_per_step": lin_launches,
             "linear_tflops": lin_flops / (lin_ms * 1e-3) / 1e12,
             "linear_mfma_util_pct": 100.0 * lin_flops / (lin_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS,
-            "output_finite": finite, "device": info.get("name"),
+            "output_finite": finite, "device": info.get("name") or info.get("arch"),
+            "host_to_host_ms_per_step": pcie_ms,
         },
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,

@@ -136,14 +136,18 @@ __global__ void where_kernel(const uint8_t* __restrict__ c, int dt_a, const void
 }
 
 // y[r, j] = round(gelu(x[r, j]) * x[r, F + j]) in f32 with one rounding to dt_y.
+// A 16-bit output takes gelu_fast, the GELU of the GEMMs' fused GeGLU
+// epilogue, so the fused and unfused paths give the same bits; f32 keeps
+// libm's erf.
 __global__ void geglu_kernel(int dt_x, const void* __restrict__ x, int64_t ldx, int dt_y, void* __restrict__ y,
                              int64_t rows, int64_t F) {
   int64_t n = rows * F;
+  const bool fast = dt_y == HB_F16 || dt_y == HB_BF16;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     int64_t r = i / F, j = i - r * F;
     float v = load_f(x, r * ldx + j, dt_x);
     float g = load_f(x, r * ldx + F + j, dt_x);
-    store_f(y, i, dt_y, gelu_erf(v) * g);
+    store_f(y, i, dt_y, (fast ? gelu_fast(v) : gelu_erf(v)) * g);
   }
 }
 

@@ -386,8 +386,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   static_assert(B_LD * NT == BN * 8 && BN % 32 == 0, "BN must be a multiple of 32");
   static_assert(!GEGLU || (TN % 2 == 0), "GEGLU needs an even number of column blocks");
 
+  constexpr int CPR = BNO / 8;           // 16-byte chunks per output row
+  constexpr int RG = (CPR + 7) / 8;      // C tile: groups of 8 chunks per row
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* Bs = smem;  // [2][BN*64]
+  uint16_t* Bs = smem;               // [2][BN*64] W tiles
+  uint16_t* Cs = smem + 2 * BN * BK;  // [RG][BM][8] 16-byte chunks: residual in, output out
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lg = lane >> 5;
@@ -482,6 +485,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     else return j * 32;
   };
 
+  // The C tile in LDS: 16-byte chunk c of tile row r sits in slot
+  // (c/8)*BM*8 + r*8 + ((c%8) ^ (r%8)).  The epilogue's 8-byte accesses of 32
+  // consecutive rows then spread over the banks, and 8 consecutive chunks of
+  // a row are 8 distinct slots of one 128-byte span.  With a residual the
+  // tile is first filled with R straight from global memory
+  // (global_load_lds_dwordx4, issued at the tile's first K stage); the
+  // epilogue adds the rounded linear output in place, and the whole tile
+  // leaves with coalesced 16-byte stores (whole rows per instruction: partial
+  // lines written from registers cost HBM write-backs twice over).
+  auto r_slot = [&](int r, int c) { return (c >> 3) * (BM * 8) + r * 8 + ((c & 7) ^ (r & 7)); };
+  // DMA instruction i of wave w fills slots (4i + w)*64 + lane, i.e. row
+  // 32*(i%8) + 8w + lane/8, chunk 8*(i/8) + ((lane%8) ^ (lane/8)).  Every lane
+  // writes its own slot, so slots outside the operand load a clamped,
+  // in-bounds address (ldr % 8 == 0: a chunk starting below N lies inside the
+  // row) and are never stored.
+  auto dma_resid = [&](int m0, int n0) {
+    int ln = lane, wv = wave;
+    asm volatile("" : "+v"(ln), "+v"(wv));  // per-tile address math, not hoisted (see the epilogue)
+    const int r_cx = (ln & 7) ^ (ln >> 3);
+    const int rbase = m0 + wv * 8 + (ln >> 3), cbase = n0 + r_cx * 8;
+#pragma unroll
+    for (int i = 0; i < RG * 8; i++) {
+      const int row = rbase + (i & 7) * 32, col = cbase + (i >> 3) * 64;
+      const bool cok = (i >> 3) * 8 + r_cx < CPR && col < N;
+      __builtin_amdgcn_global_load_lds((const void*)(R + (int64_t)(row < M ? row : M - 1) * ldr + (cok ? col : 0)),
+                                       (__attribute__((address_space(3))) void*)(Cs + (i * 4 + wv) * 512), 16, 0,
+                                       0);
+    }
+  };
+
   float16v acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
@@ -490,65 +523,76 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  // ---- epilogue from registers: bias, one rounding, GeGLU (value block j,
-  // gate block j + TN/2 hold the same output columns), residual; leaves the
-  // accumulators zeroed for the next tile
-  auto epilogue = [&](int m0, int n0) {
-    constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
+  // ---- epilogue: bias, one rounding to the storage type, GeGLU (value
+  // block j and gate block j + TN/2 hold the same output columns), then the
+  // residual add, y = round(round(x.w^T + b) + r), into the C tile
+  constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
+  // The lane indices are re-read through an empty asm inside the epilogue,
+  // the write-out and the residual DMA: the compiler then computes their
+  // per-lane addresses there, once per tile, instead of hoisting all of them
+  // out of the tile loop and spilling them to scratch (an HBM write per
+  // spilled register).
+  auto epilogue = [&](int n0) {
+    int l32 = lane & 31, lg = lane >> 5, wv = wave;
+    asm volatile("" : "+v"(l32), "+v"(lg), "+v"(wv));
 #pragma unroll
     for (int j = 0; j < OUT_TN; j++) {
 #pragma unroll
       for (int g = 0; g < 4; g++) {
-        const int ncol = n0 + j * 32 + 8 * g + 4 * lg;
+        const int col = j * 32 + 8 * g + 4 * lg;  // tile output column of element 0
         float bv[4] = {0.f, 0.f, 0.f, 0.f}, bg[4] = {0.f, 0.f, 0.f, 0.f};
         if (bias != nullptr) {
 #pragma unroll
           for (int e = 0; e < 4; e++)
-            if (ncol + e < N) {
-              bv[e] = to_f<BF16>(bias[ncol + e]);
-              if constexpr (GEGLU) bg[e] = to_f<BF16>(bias[N + ncol + e]);
+            if (n0 + col + e < N) {
+              bv[e] = to_f<BF16>(bias[n0 + col + e]);
+              if constexpr (GEGLU) bg[e] = to_f<BF16>(bias[N + n0 + col + e]);
             }
         }
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-          const int mrow = m0 + wave * 64 + i * 32 + l32;
           uint16_t o[4];
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            float v = to_f<BF16>(from_f<BF16>(acc[i][j][4 * g + e] + bv[e]));
             if constexpr (GEGLU) {
+              const float v = to_f<BF16>(from_f<BF16>(acc[i][j][4 * g + e] + bv[e]));
               const float gt = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][4 * g + e] + bg[e]));
-              v = gelu_fast(v) * gt;
-            }
-            o[e] = from_f<BF16>(v);
-          }
-          if (mrow < M && ncol < N) {
-            uint16_t* yp = Y + (int64_t)mrow * ldy + ncol;
-            const uint16_t* rp = R != nullptr ? R + (int64_t)mrow * ldr + ncol : nullptr;
-            if (ncol + 4 <= N) {
-              if (rp != nullptr) {
-                const uint2v rv = *(const uint2v*)rp;
-                const uint16_t rr[4] = {(uint16_t)(rv.x & 0xffff), (uint16_t)(rv.x >> 16),
-                                        (uint16_t)(rv.y & 0xffff), (uint16_t)(rv.y >> 16)};
-#pragma unroll
-                for (int e = 0; e < 4; e++) o[e] = from_f<BF16>(to_f<BF16>(o[e]) + to_f<BF16>(rr[e]));
-              }
-              *(uint2v*)yp =
-                  uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+              o[e] = from_f<BF16>(gelu_fast(v) * gt);
             } else {
-              for (int e = 0; e < 4 && ncol + e < N; e++)
-                yp[e] = rp != nullptr ? from_f<BF16>(to_f<BF16>(o[e]) + to_f<BF16>(rp[e])) : o[e];
+              o[e] = from_f<BF16>(acc[i][j][4 * g + e] + bv[e]);
             }
           }
+          uint2v* cp = (uint2v*)(Cs + r_slot(wv * 64 + i * 32 + l32, col >> 3) * 8 + (col & 7));
+          if (R != nullptr) {
+            const uint2v rv = *cp;
+            const uint16_t rr[4] = {(uint16_t)(rv.x & 0xffff), (uint16_t)(rv.x >> 16), (uint16_t)(rv.y & 0xffff),
+                                    (uint16_t)(rv.y >> 16)};
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = from_f<BF16>(to_f<BF16>(o[e]) + to_f<BF16>(rr[e]));
+          }
+          *cp = uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int j = 0; j < TN; j++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+  };
+  // the C tile -> Y: thread t takes chunks t, t + 256, ...; consecutive
+  // threads cover consecutive 16-byte pieces of a row
+  auto write_out = [&](int m0, int n0) {
+    int t0 = tid;
+    asm volatile("" : "+v"(t0));
+    for (int q = t0; q < BM * CPR; q += NT) {
+      const int r = q / CPR, c = q - r * CPR;
+      const int gm = m0 + r, gn = n0 + c * 8;
+      if (gm >= M || gn >= N) continue;
+      const uint4v v = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+      uint16_t* yp = Y + (int64_t)gm * ldy + gn;
+      if (gn + 8 <= N) {
+        *(uint4v*)yp = v;
+      } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        for (int e = 0; gn + e < N; e++) yp[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      }
+    }
   };
 
   uint4v A0[TM][KS], A1[TM][KS], A2[TM][KS];
@@ -556,6 +600,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // step g: MFMAs on `ac` and LDS buffer g&1; loads stage g+2 of the stream
   // into (al, bl); stages the W tile of g+1 (held in bs) into the other buffer.
   auto step = [&](int g, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl, BRegs& bs) {
+    if (R != nullptr) {  // the residual tile arrives while the tile computes
+      const int it = g / KT;
+      if (g == it * KT) dma_resid(tile_m0(it), tile_n0(it));
+    }
     const int g2 = g + 2 < S ? g + 2 : S - 1;
     const int i2 = g2 / KT, k2 = (g2 - i2 * KT) * BK;
     load_a(tile_m0(i2), k2, al);
@@ -610,7 +658,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if (kt + 4 < KT) step(g0 + kt + 4, A1, A0, B0, B1);
       if (kt + 5 < KT) step(g0 + kt + 5, A2, A1, B1, B0);
     }
-    epilogue(tile_m0(it), tile_n0(it));
+    // the residual DMA of the tile's first stage has landed once at most the
+    // W and A loads of one stage are outstanding (they were all issued after
+    // it, and loads complete in order); the barrier makes every wave's part
+    // of the C tile visible (and, without R, keeps the previous tile's
+    // write-out reads ahead of this epilogue's writes)
+    static_assert(TM * KS + B_LD <= 15, "vmcnt immediate");
+    if (R != nullptr) __builtin_amdgcn_s_waitcnt(0x0F70 | (TM * KS + B_LD));
+    __syncthreads();
+    epilogue(tile_n0(it));
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+    __syncthreads();
+    write_out(tile_m0(it), tile_n0(it));
+    if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
   }
 }
 
@@ -733,7 +798,8 @@ static void launch_arow(hipStream_t st, int cus, const uint16_t* x, int64_t ldx,
   const int KT = (K + 63) / 64;
   int grid = KT % 6 == 0 ? (tiles < cus ? tiles : cus) / 8 * 8 : (tiles + 7) / 8 * 8;
   HB_REQUIRE(grid >= 8, "hb_linear: large-M GEMM needs at least 8 tiles");
-  const size_t lds = (size_t)2 * BN * 64 * sizeof(uint16_t);
+  constexpr int RG = (BNO / 8 + 7) / 8;
+  const size_t lds = ((size_t)2 * BN * 64 + (size_t)RG * 256 * 64) * sizeof(uint16_t);
   auto kern = gemm_mfma_arow<BN, BF16, GEGLU, QB, AFF, SF32, KTAIL>;
   static bool attr = false;
   if (!attr) {

@@ -99,6 +99,23 @@ def test_linear_geglu_bias_ragged(b, dtype):
             b.dispose(t)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_fused_geglu_is_bit_identical_to_separate_geglu(b, dtype):
+    """linear -> geglu fused into the GEMM epilogue gives the same bits as a
+    materialised linear followed by the standalone GeGLU kernel."""
+    rng = np.random.default_rng(10)
+    for M in (300, 4096):
+        x = rounded(rng.standard_normal((M, 768)), dtype)
+        w = rounded(rng.normal(0, 0.05, (2304, 768)), dtype)
+        X, Wt = b.fromHost(to_host(x, dtype)), b.fromHost(to_host(w, dtype))
+        fused = b.read(b.geglu(b.linear(X, Wt))).data
+        sep = b.read(b.geglu(b._ready(b.linear(X, Wt)))).data
+        assert b.stats["linear_fused_geglu"] > 0
+        np.testing.assert_array_equal(fused, sep)
+        b.dispose(X)
+        b.dispose(Wt)
+
+
 def test_linear_f32_path(b):
     rng = np.random.default_rng(8)
     x = rng.standard_normal((70, 45)).astype(np.float32)
