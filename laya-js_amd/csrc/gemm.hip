@@ -395,15 +395,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lg = lane >> 5;
 
-  // this block's tiles: c0 + slot + i * nx for i < ntile (gridDim.x % 8 == 0)
+  // This block's tiles (gridDim.x % 8 == 0).  XCD x owns the row panels
+  // [mb0, mb1) with every column tile, and its blocks take the panel's tiles
+  // column-tile-major: local tile l = slot + i * nx is row panel mb0 + l % mx,
+  // column tile l / mx.  The tiles one XCD computes at a time then share a
+  // few column tiles of W and cycle over the XCD's own rows of X, which stay
+  // in its L2 from one column tile to the next.
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, nx = gridDim.x >> 3;
-  const int c0 = (int)((int64_t)xcd * tiles / 8), c1 = (int)((int64_t)(xcd + 1) * tiles / 8);
-  const int ntile = c1 - c0 > slot ? (c1 - c0 - slot + nx - 1) / nx : 0;
+  const int tiles_m = tiles / tiles_n;
+  const int mb0 = xcd * tiles_m / 8, mx = (xcd + 1) * tiles_m / 8 - mb0;
+  const int nloc = mx * tiles_n;
+  const int ntile = nloc > slot ? (nloc - slot + nx - 1) / nx : 0;
   if (ntile == 0) return;
   const int KT = (K + BK - 1) / BK;
   const int S = ntile * KT;  // stages in this block's stream
-  auto tile_m0 = [&](int i) { return ((c0 + slot + i * nx) / tiles_n) * BM; };
-  auto tile_n0 = [&](int i) { return ((c0 + slot + i * nx) % tiles_n) * BNO; };
+  auto tile_m0 = [&](int i) { return (mb0 + (slot + i * nx) % mx) * BM; };
+  auto tile_n0 = [&](int i) { return ((slot + i * nx) / mx) * BNO; };
 
   // Loads are branch-free: addresses are clamped into the operand.  Rows past
   // M (A) or N (W) only feed outputs that are never stored, so they need no
@@ -794,9 +801,10 @@ static void launch_arow(hipStream_t st, int cus, const uint16_t* x, int64_t ldx,
   constexpr int BNO = GEGLU ? BN / 2 : BN;
   const int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO, tiles = tiles_m * tiles_n;
   // one persistent block per CU, a multiple of 8 (one per XCD); with
-  // K % 384 != 0 one block per tile
+  // K % 384 != 0 at most one tile per block: every XCD gets as many blocks
+  // as the largest XCD share of tiles (ceil(tiles_m / 8) row panels)
   const int KT = (K + 63) / 64;
-  int grid = KT % 6 == 0 ? (tiles < cus ? tiles : cus) / 8 * 8 : (tiles + 7) / 8 * 8;
+  int grid = KT % 6 == 0 ? (tiles < cus ? tiles : cus) / 8 * 8 : 8 * (((tiles_m + 7) / 8) * tiles_n);
   HB_REQUIRE(grid >= 8, "hb_linear: large-M GEMM needs at least 8 tiles");
   constexpr int RG = (BNO / 8 + 7) / 8;
   const size_t lds = ((size_t)2 * BN * 64 + (size_t)RG * 256 * 64) * sizeof(uint16_t);
