@@ -155,7 +155,10 @@ __device__ __forceinline__ float gelu_fast(float x) {
   p = fmaf(t, p, 1.421413741f);
   p = fmaf(t, p, -0.284496736f);
   p = fmaf(t, p, 0.254829592f);
-  const float pe = p * t * __expf(-z * z);  // 1 - erf(z)
+  float pe = p * t * __expf(-z * z);  // 1 - erf(z)
+  // pinned: no contraction of p*t*e into the subtraction below, so every
+  // caller rounds the same way whatever code surrounds it
+  pe = pin_f32(pe);
   return 0.5f * x * (x >= 0.f ? 2.0f - pe : pe);
 }
 

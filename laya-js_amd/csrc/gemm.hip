@@ -25,6 +25,7 @@
 // gemm_simt is the f32 path (and the fallback for shapes the MFMA kernel's
 // 16-byte loads cannot take: K or row strides not a multiple of 8).
 #include <stdexcept>
+#include <type_traits>
 
 #include "common.h"
 
@@ -385,6 +386,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   constexpr int BNO = GEGLU ? BN / 2 : BN;
   static_assert(B_LD * NT == BN * 8 && BN % 32 == 0, "BN must be a multiple of 32");
   static_assert(!GEGLU || (TN % 2 == 0), "GEGLU needs an even number of column blocks");
+  static_assert((BM * (BNO / 8)) % NT == 0, "write-out assumes whole rounds of chunks");
 
   constexpr int CPR = BNO / 8;           // 16-byte chunks per output row
   constexpr int RG = (CPR + 7) / 8;      // C tile: groups of 8 chunks per row
@@ -539,7 +541,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // per-lane addresses there, once per tile, instead of hoisting all of them
   // out of the tile loop and spilling them to scratch (an HBM write per
   // spilled register).
-  auto epilogue = [&](int n0) {
+  auto epilogue = [&](int n0, auto has_bias, auto has_r) {
+    constexpr bool HB = decltype(has_bias)::value, HR = decltype(has_r)::value;
     int l32 = lane & 31, lg = lane >> 5, wv = wave;
     asm volatile("" : "+v"(l32), "+v"(lg), "+v"(wv));
 #pragma unroll
@@ -548,7 +551,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int g = 0; g < 4; g++) {
         const int col = j * 32 + 8 * g + 4 * lg;  // tile output column of element 0
         float bv[4] = {0.f, 0.f, 0.f, 0.f}, bg[4] = {0.f, 0.f, 0.f, 0.f};
-        if (bias != nullptr) {
+        if constexpr (HB) {
 #pragma unroll
           for (int e = 0; e < 4; e++)
             if (n0 + col + e < N) {
@@ -561,16 +564,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           uint16_t o[4];
 #pragma unroll
           for (int e = 0; e < 4; e++) {
+            const float a = HB ? acc[i][j][4 * g + e] + bv[e] : acc[i][j][4 * g + e];
             if constexpr (GEGLU) {
-              const float v = to_f<BF16>(from_f<BF16>(acc[i][j][4 * g + e] + bv[e]));
-              const float gt = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][4 * g + e] + bg[e]));
-              o[e] = from_f<BF16>(gelu_fast(v) * gt);
+              const float ag = HB ? acc[i][j + TN / 2][4 * g + e] + bg[e] : acc[i][j + TN / 2][4 * g + e];
+              o[e] = from_f<BF16>(gelu_fast(to_f<BF16>(from_f<BF16>(a))) * to_f<BF16>(from_f<BF16>(ag)));
             } else {
-              o[e] = from_f<BF16>(acc[i][j][4 * g + e] + bv[e]);
+              o[e] = from_f<BF16>(a);
             }
           }
           uint2v* cp = (uint2v*)(Cs + r_slot(wv * 64 + i * 32 + l32, col >> 3) * 8 + (col & 7));
-          if (R != nullptr) {
+          if constexpr (HR) {
             const uint2v rv = *cp;
             const uint16_t rr[4] = {(uint16_t)(rv.x & 0xffff), (uint16_t)(rv.x >> 16), (uint16_t)(rv.y & 0xffff),
                                     (uint16_t)(rv.y >> 16)};
@@ -587,6 +590,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto write_out = [&](int m0, int n0) {
     int t0 = tid;
     asm volatile("" : "+v"(t0));
+    if (m0 + BM <= M && n0 + BNO <= N) {  // interior tile: no bounds checks
+      uint16_t* yb = Y + (int64_t)m0 * ldy + n0;
+#pragma unroll
+      for (int k = 0; k < BM * CPR / NT; k++) {
+        const int q = t0 + k * NT, r = q / CPR, c = q - r * CPR;
+        *(uint4v*)(yb + (int64_t)r * ldy + c * 8) = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+      }
+      return;
+    }
     for (int q = t0; q < BM * CPR; q += NT) {
       const int r = q / CPR, c = q - r * CPR;
       const int gm = m0 + r, gn = n0 + c * 8;
@@ -673,7 +685,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     static_assert(TM * KS + B_LD <= 15, "vmcnt immediate");
     if (R != nullptr) __builtin_amdgcn_s_waitcnt(0x0F70 | (TM * KS + B_LD));
     __syncthreads();
-    epilogue(tile_n0(it));
+    {
+      using T = std::true_type;
+      using F = std::false_type;
+      const int n0 = tile_n0(it);
+      if (bias == nullptr) {
+        if (R == nullptr) epilogue(n0, F{}, F{});
+        else epilogue(n0, F{}, T{});
+      } else {
+        if (R == nullptr) epilogue(n0, T{}, F{});
+        else epilogue(n0, T{}, T{});
+      }
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
