@@ -134,19 +134,30 @@ __device__ __forceinline__ void load_pair(const uint16_t* __restrict__ src, bool
   }
 }
 
-// Rotates a loaded chunk pair by RoPE at position `pos` (when `tab` is set),
+// cos / sin of the 8 rotation pairs (d, d + 32), d in [8c, 8c+8), at
+// position `pos` of a RoPE table [L][32] (float2).
+__device__ __forceinline__ void load_cs(const float2* __restrict__ tab, int pos, int c, float2 (&cs)[8]) {
+  const float4v* t = (const float4v*)(tab + pos * 32 + c * 8);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float4v v = t[e];
+    cs[2 * e] = float2{v[0], v[1]};
+    cs[2 * e + 1] = float2{v[2], v[3]};
+  }
+}
+
+// Rotates a loaded chunk pair by RoPE (when `rot`) with the pairs' cos / sin,
 // rounding to the storage type like a separate Backend.rope, and writes it
 // to the swizzled [rows][64] LDS tile.
 template <bool BF16>
-__device__ __forceinline__ void store_pair(uint4v lo, uint4v hi, bool valid, int c, const float2* __restrict__ tab,
-                                           int pos, uint16_t* lds, int row) {
-  if (valid && tab != nullptr) {
-    const float2* t = tab + pos * 32 + c * 8;
+__device__ __forceinline__ void store_pair(uint4v lo, uint4v hi, bool rot, int c, const float2 (&cs)[8],
+                                           uint16_t* lds, int row) {
+  if (rot) {
     uint32_t* l = (uint32_t*)&lo;
     uint32_t* h = (uint32_t*)&hi;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      float2 c0 = t[2 * e], c1 = t[2 * e + 1];
+      const float2 c0 = cs[2 * e], c1 = cs[2 * e + 1];
       float x0a = tof<BF16>(l[e] & 0xffff), x0b = tof<BF16>(l[e] >> 16);
       float x1a = tof<BF16>(h[e] & 0xffff), x1b = tof<BF16>(h[e] >> 16);
       uint32_t oa = fromf<BF16>(pin_f32(fmaf(-x1a, c0.y, x0a * c0.x)));
@@ -162,7 +173,7 @@ __device__ __forceinline__ void store_pair(uint4v lo, uint4v hi, bool valid, int
 }
 
 template <bool BF16>
-__global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q, S4 qs, const uint16_t* __restrict__ K,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void sdpa_mfma(const uint16_t* __restrict__ Q, S4 qs, const uint16_t* __restrict__ K,
                                                  S4 ks, const uint16_t* __restrict__ V, S4 vs,
                                                  const uint8_t* __restrict__ mask, S4 ms, int mask_vec,
                                                  const uint8_t* __restrict__ cls, uint16_t* __restrict__ O, S4 os,
@@ -196,14 +207,77 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
     while (kt < nkt && tile_class(kt) == 0) kt++;
     return kt;
   };
+  __syncthreads();  // the class row is complete
 
-  // ---- stage Q (rotated) and build this wave's B fragments of Q^T
-  for (int t = tid; t < kBQ * 4; t += 256) {
-    int r = t >> 2, c = t & 3;
-    int q = q0 + r;
-    uint4v lo, hi;
-    load_pair(Qb + (int64_t)q * qs.s[2], q < Lq, c, lo, hi);
-    store_pair<BF16>(lo, hi, q < Lq, c, tabq, q, Qs, r);
+  // this thread's share of a K tile (row kr, chunk pair kc) and V tile
+  // (key pair vj, chunk vc), prefetched into registers one tile ahead
+  const int kr = tid >> 2, kc = tid & 3;
+  const int vc = tid & 7, vj = 2 * (tid >> 3);
+  uint4v klo, khi, va, vb;
+  float2 kcs[8];  // RoPE cos / sin of this thread's K row (fused RoPE)
+  auto prefetch = [&](int kt) {
+    const int k0 = kt * kBK;
+    load_pair(Kb + (int64_t)(k0 + kr) * ks.s[2], k0 + kr < Lk, kc, klo, khi);
+    if (tabk != nullptr && k0 + kr < Lk) load_cs(tabk, k0 + kr, kc, kcs);
+    va = uint4v{0, 0, 0, 0};
+    vb = uint4v{0, 0, 0, 0};
+    if (k0 + vj < Lk) va = *(const uint4v*)(Vb + (int64_t)(k0 + vj) * vs.s[2] + vc * 8);
+    if (k0 + vj + 1 < Lk) vb = *(const uint4v*)(Vb + (int64_t)(k0 + vj + 1) * vs.s[2] + vc * 8);
+  };
+
+  // this lane's mask bytes of a tile: 8 contiguous keys for each of its two
+  // queries (qb) and halves (t)
+  auto load_mask = [&](int kt, uint2v (&mw)[2][2]) {
+    const int k0 = kt * kBK;
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+      const int q = q0 + wave * 32 + qb * 16 + li;
+      const uint8_t* mrow = mask + b * ms.s[0] + (int64_t)(q < Lq ? q : 0) * ms.s[2];
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const int kbase = k0 + 32 * t + 8 * g;
+        if (mask_vec && kbase + 8 <= Lk) {
+          mw[qb][t] = *(const uint2v*)(mrow + kbase);
+        } else {
+          uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            uint32_t bit = (kbase + e < Lk) ? (mrow[(int64_t)(kbase + e) * ms.s[3]] != 0) : 0u;
+            if (e < 4) w0 |= bit << (8 * e);
+            else w1 |= bit << (8 * (e - 4));
+          }
+          mw[qb][t] = uint2v{w0, w1};
+        }
+      }
+    }
+  };
+
+  // the first K / V tile (and its mask bytes) is requested before Q is
+  // staged, so the two loads' latencies overlap
+  int kt = next_tile(-1);
+  uint2v mw[2][2], mwn[2][2];
+  if (kt < nkt) {
+    prefetch(kt);
+    if (mask != nullptr && tile_class(kt) == 2) load_mask(kt, mw);
+  }
+
+  static_assert(kBQ * 4 == 2 * 256, "Q staging: two rounds of 256 threads");
+  // ---- stage Q (rotated) and build this wave's B fragments of Q^T; both
+  // rounds of loads are issued before the first store
+  {
+    uint4v lo[2], hi[2];
+    float2 cs[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int t = tid + u * 256, r = t >> 2, c = t & 3, q = q0 + r;
+      load_pair(Qb + (int64_t)q * qs.s[2], q < Lq, c, lo[u], hi[u]);
+      if (tabq != nullptr && q < Lq) load_cs(tabq, q, c, cs[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int t = tid + u * 256, r = t >> 2, c = t & 3, q = q0 + r;
+      store_pair<BF16>(lo[u], hi[u], tabq != nullptr && q < Lq, c, cs[u], Qs, r);
+    }
   }
   __syncthreads();
   uint4v qf[2][2];
@@ -212,6 +286,7 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
 #pragma unroll
     for (int s = 0; s < 2; s++) qf[qb][s] = *(const uint4v*)(Qs + qk_swz(wave * 32 + qb * 16 + li, s * 4 + g));
 
+
   float4v o[2][4];
 #pragma unroll
   for (int qb = 0; qb < 2; qb++)
@@ -219,27 +294,42 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
     for (int d = 0; d < 4; d++) o[qb][d] = float4v{0.f, 0.f, 0.f, 0.f};
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
 
-  // this thread's share of a K tile (row kr, chunk pair kc) and V tile
-  // (key pair vj, chunk vc), prefetched into registers one tile ahead
-  const int kr = tid >> 2, kc = tid & 3;
-  const int vc = tid & 7, vj = 2 * (tid >> 3);
-  uint4v klo, khi, va, vb;
-  auto prefetch = [&](int kt) {
-    const int k0 = kt * kBK;
-    load_pair(Kb + (int64_t)(k0 + kr) * ks.s[2], k0 + kr < Lk, kc, klo, khi);
-    va = uint4v{0, 0, 0, 0};
-    vb = uint4v{0, 0, 0, 0};
-    if (k0 + vj < Lk) va = *(const uint4v*)(Vb + (int64_t)(k0 + vj) * vs.s[2] + vc * 8);
-    if (k0 + vj + 1 < Lk) vb = *(const uint4v*)(Vb + (int64_t)(k0 + vj + 1) * vs.s[2] + vc * 8);
+  // online softmax of one 64-key tile for query block qb: scores sv (raw,
+  // -inf where hidden) -> P fragments, running max / sum, O rescale
+  uint4v pf[2][2];
+  auto softmax = [&](int qb, float (&sv)[2][8], float mx) {
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(m[qb], mx);  // raw (unscaled) row max
+    const float mc = mnew == -INFINITY ? 0.f : mnew * scale_log2;
+    const float alpha = __builtin_amdgcn_exp2f(m[qb] * scale_log2 - mc);
+    m[qb] = mnew;
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[t][e], scale_log2, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[t][e + 1], scale_log2, -mc));
+        psum += p0 + p1;
+        pk[e >> 1] = pack2<BF16>(p0, p1);
+      }
+      pf[qb][t] = uint4v{pk[0], pk[1], pk[2], pk[3]};
+    }
+    l[qb] = l[qb] * alpha + psum;
+    // rescale O only when some row max of this wave moved
+    if (!__all(alpha == 1.0f)) {
+#pragma unroll
+      for (int d = 0; d < 4; d++) o[qb][d] *= alpha;
+    }
   };
 
-  int kt = next_tile(-1);
-  if (kt < nkt) prefetch(kt);
   while (kt < nkt) {
     const int k0 = kt * kBK;
     const int cl = tile_class(kt);
     __syncthreads();  // the previous tile's K / V^T reads are done
-    store_pair<BF16>(klo, khi, k0 + kr < Lk, kc, tabk, k0 + kr, Ks, kr);
+    store_pair<BF16>(klo, khi, tabk != nullptr && k0 + kr < Lk, kc, kcs, Ks, kr);
     {
       const uint32_t* pa = (const uint32_t*)&va;
       const uint32_t* pb = (const uint32_t*)&vb;
@@ -253,34 +343,12 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
     }
     __syncthreads();
 
-    // mask bytes of this tile (issued before the next tile's prefetch, so
-    // waiting for them does not wait for the prefetch)
-    uint2v mw[2][2];
-    if (cl == 2 && mask != nullptr) {
-#pragma unroll
-      for (int qb = 0; qb < 2; qb++) {
-        const int q = q0 + wave * 32 + qb * 16 + li;
-        const uint8_t* mrow = mask + b * ms.s[0] + (int64_t)(q < Lq ? q : 0) * ms.s[2];
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-          const int kbase = k0 + 32 * t + 8 * g;
-          if (mask_vec && kbase + 8 <= Lk) {
-            mw[qb][t] = *(const uint2v*)(mrow + kbase);
-          } else {
-            uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-              uint32_t bit = (kbase + e < Lk) ? (mrow[(int64_t)(kbase + e) * ms.s[3]] != 0) : 0u;
-              if (e < 4) w0 |= bit << (8 * e);
-              else w1 |= bit << (8 * (e - 4));
-            }
-            mw[qb][t] = uint2v{w0, w1};
-          }
-        }
-      }
-    }
+    // next tile's K / V (and mask bytes) one tile ahead
     const int nk = next_tile(kt);
-    if (nk < nkt) prefetch(nk);
+    if (nk < nkt) {
+      prefetch(nk);
+      if (mask != nullptr && tile_class(nk) == 2) load_mask(nk, mwn);
+    }
 
     // ---- S^T = K . Q^T over 4 key blocks; block kb row i holds key
     // 32*(kb/2) + 8*(i/4) + (i%4) + 4*(kb%2) so a lane's 8 keys are contiguous
@@ -298,55 +366,44 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
       }
     }
 
-    // ---- mask, online softmax (log2 domain, scale folded into one fma), P fragments
-    const bool in_range = k0 + kBK <= Lk;
-    uint4v pf[2][2];
+    // ---- mask (only for mixed tiles), online softmax, P fragments
+    if (cl == 1) {
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-      float sv[2][8];
-      float mx = -INFINITY;
+      for (int qb = 0; qb < 2; qb++) {
+        float sv[2][8];
+        float mx = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < 2; t++) {
-        const int kbase = k0 + 32 * t + 8 * g;  // this lane's 8 contiguous keys
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float s = e < 4 ? st[qb][2 * t][e] : st[qb][2 * t + 1][e - 4];
-          bool vis = true;
-          if (cl == 2) {
+          for (int e = 0; e < 8; e++) {
+            sv[t][e] = e < 4 ? st[qb][2 * t][e] : st[qb][2 * t + 1][e - 4];
+            mx = fmaxf(mx, sv[t][e]);
+          }
+        softmax(qb, sv, mx);
+      }
+    } else {
+      const bool in_range = k0 + kBK <= Lk;
+#pragma unroll
+      for (int qb = 0; qb < 2; qb++) {
+        float sv[2][8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          const int kbase = k0 + 32 * t + 8 * g;  // this lane's 8 contiguous keys
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const float sc = e < 4 ? st[qb][2 * t][e] : st[qb][2 * t + 1][e - 4];
+            bool vis = true;
             if (mask != nullptr) {
               const uint32_t w = e < 4 ? mw[qb][t].x : mw[qb][t].y;
               vis = ((w >> (8 * (e & 3))) & 0xffu) != 0;
             }
             if (!in_range) vis = vis && (kbase + e) < Lk;
+            sv[t][e] = vis ? sc : -INFINITY;
+            mx = fmaxf(mx, sv[t][e]);
           }
-          sv[t][e] = vis ? s : -INFINITY;
-          mx = fmaxf(mx, sv[t][e]);
         }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m[qb], mx);                       // raw (unscaled) row max
-      const float mc = mnew == -INFINITY ? 0.f : mnew * scale_log2;
-      const float alpha = __builtin_amdgcn_exp2f(m[qb] * scale_log2 - mc);
-      m[qb] = mnew;
-      float psum = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; t++) {
-        uint32_t pk[4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[t][e], scale_log2, -mc));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[t][e + 1], scale_log2, -mc));
-          psum += p0 + p1;
-          pk[e >> 1] = pack2<BF16>(p0, p1);
-        }
-        pf[qb][t] = uint4v{pk[0], pk[1], pk[2], pk[3]};
-      }
-      l[qb] = l[qb] * alpha + psum;
-      // rescale O only when some row max of this wave moved
-      if (!__all(alpha == 1.0f)) {
-#pragma unroll
-        for (int d = 0; d < 4; d++) o[qb][d] *= alpha;
+        softmax(qb, sv, mx);
       }
     }
 
@@ -360,6 +417,10 @@ __global__ __launch_bounds__(256) void sdpa_mfma(const uint16_t* __restrict__ Q,
         for (int qb = 0; qb < 2; qb++) o[qb][d] = mfma16<BF16>(vf, pf[qb][t], o[qb][d]);
       }
     }
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+      for (int t = 0; t < 2; t++) mw[qb][t] = mwn[qb][t];
     kt = nk;
   }
 
