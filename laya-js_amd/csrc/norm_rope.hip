@@ -1,5 +1,6 @@
 // LayerNorm (wave-per-row, f32 two-pass statistics) and split-half RoPE.
 #include <stdexcept>
+#include <type_traits>
 
 #include "common.h"
 
@@ -9,56 +10,76 @@ const float* rope_table(uintptr_t ctx, int64_t L, int64_t D, double base);
 
 // One wave per row; each lane keeps its 4-element groups in registers, so
 // the row is read from HBM once and written once (2 x 2 x D bytes per row).
-template <int G>
-__global__ __launch_bounds__(256) void layernorm_vec_kernel(int dt_x, const uint16_t* __restrict__ x, int64_t ldx,
-                                                            int dt_w, const void* __restrict__ w,
-                                                            const void* __restrict__ b, int dt_y,
-                                                            uint16_t* __restrict__ y, int64_t rows, int D,
-                                                            float eps) {
-  int lane = threadIdx.x & 63;
-  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// x and y share the 16-bit type BF (f16 / bf16); the affine parameters are of
+// type PK (0: none, 1: f16, 2: bf16, 3: f32) and are read 4 at a time.
+template <int PK>
+__device__ __forceinline__ void load4_param(const void* p, int c, float (&v)[4]) {
+  if constexpr (PK == 3) {
+    const float4v f = *(const float4v*)((const float*)p + c);
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = f[e];
+  } else {
+    const uint2v raw = *(const uint2v*)((const uint16_t*)p + c);
+    const uint16_t h[4] = {(uint16_t)(raw.x & 0xffff), (uint16_t)(raw.x >> 16), (uint16_t)(raw.y & 0xffff),
+                           (uint16_t)(raw.y >> 16)};
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = PK == 1 ? f16_bits_to_f32(h[e]) : bf16_to_f32(h[e]);
+  }
+}
+
+template <int G, bool BF, int PK>
+__global__ __launch_bounds__(256) void layernorm_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                            const void* __restrict__ w, const void* __restrict__ b,
+                                                            uint16_t* __restrict__ y, int64_t rows, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const uint16_t* xr = x + row * ldx;
+  uint2v raw[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) raw[g] = *(const uint2v*)(xr + (g * 64 + lane) * 4);
   float v[G][4];
   float s = 0.0f;
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    int c = (g * 64 + lane) * 4;
-    uint2v raw = *(const uint2v*)(xr + c);
-    uint16_t h[4] = {(uint16_t)(raw.x & 0xffff), (uint16_t)(raw.x >> 16), (uint16_t)(raw.y & 0xffff),
-                     (uint16_t)(raw.y >> 16)};
+    const uint16_t h[4] = {(uint16_t)(raw[g].x & 0xffff), (uint16_t)(raw[g].x >> 16), (uint16_t)(raw[g].y & 0xffff),
+                           (uint16_t)(raw[g].y >> 16)};
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      v[g][e] = dt_x == HB_F16 ? f16_bits_to_f32(h[e]) : bf16_to_f32(h[e]);
+      v[g][e] = BF ? bf16_to_f32(h[e]) : f16_bits_to_f32(h[e]);
       s += v[g][e];
     }
   }
-  float mean = wave_sum(s) / (float)D;
+  const float mean = wave_sum(s) / (float)D;
   float q = 0.0f;
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      float d = v[g][e] - mean;
+      const float d = v[g][e] - mean;
       q += d * d;
     }
-  float rstd = 1.0f / sqrtf(wave_sum(q) / (float)D + eps);
+  const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)D + eps);
   uint16_t* yr = y + row * (int64_t)D;
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    int c = (g * 64 + lane) * 4;
+    const int c = (g * 64 + lane) * 4;
+    float wv[4] = {1.f, 1.f, 1.f, 1.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (PK != 0) {
+      if (w) load4_param<PK>(w, c, wv);
+      if (b) load4_param<PK>(b, c, bv);
+    }
     uint16_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       float t = (v[g][e] - mean) * rstd;
-      if (w) t *= load_f(w, c + e, dt_w);
-      if (b) t += load_f(b, c + e, dt_w);
-      o[e] = dt_y == HB_F16 ? f32_to_f16_bits(t) : f32_to_bf16(t);
+      if constexpr (PK != 0) {
+        if (w) t = pin_f32(t * wv[e]);
+        if (b) t += bv[e];
+      }
+      o[e] = BF ? f32_to_bf16(t) : f32_to_f16_bits(t);
     }
-    uint2v out;
-    out.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
-    out.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
-    *(uint2v*)(yr + c) = out;
+    *(uint2v*)(yr + c) = uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
   }
 }
 
@@ -122,27 +143,37 @@ int hb_layernorm(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt_w, ui
   if (rows == 0) return 0;
   hipStream_t st = stream_of(ctx);
   unsigned grid = (unsigned)((rows + 3) / 4);
-  bool vec = (dt_x == HB_F16 || dt_x == HB_BF16) && (dt_y == HB_F16 || dt_y == HB_BF16) && D % 256 == 0 &&
-             D <= 2048 && ldx % 4 == 0 && x % 8 == 0 && y % 8 == 0;
+  const int pk = (w == 0 && b == 0) ? 0 : dt_w == HB_F16 ? 1 : dt_w == HB_BF16 ? 2 : dt_w == HB_F32 ? 3 : -1;
+  const int64_t pal = pk == 3 ? 16 : 8;  // parameter alignment the 4-wide loads need
+  bool vec = (dt_x == HB_F16 || dt_x == HB_BF16) && dt_y == dt_x && D % 256 == 0 && D <= 2048 && ldx % 4 == 0 &&
+             x % 8 == 0 && y % 8 == 0 && pk >= 0 && w % pal == 0 && b % pal == 0;
   if (vec) {
-    int G = (int)(D / 256);
-#define LN_CASE(g)                                                                                                \
-  case g:                                                                                                         \
-    layernorm_vec_kernel<g><<<grid, 256, 0, st>>>(dt_x, (const uint16_t*)x, ldx, dt_w, (const void*)w,          \
-                                                  (const void*)b, dt_y, (uint16_t*)y, rows, (int)D, eps);         \
-    break;
-    switch (G) {
-      LN_CASE(1)
-      LN_CASE(2)
-      LN_CASE(3)
-      LN_CASE(4)
-      LN_CASE(5)
-      LN_CASE(6)
-      LN_CASE(7)
-      LN_CASE(8)
-      default: break;
+    const int G = (int)(D / 256);
+    const bool bf = dt_x == HB_BF16;
+    auto launch = [&](auto gc, auto pc) {
+      constexpr int GG = decltype(gc)::value, PP = decltype(pc)::value;
+      auto kern = bf ? layernorm_vec_kernel<GG, true, PP> : layernorm_vec_kernel<GG, false, PP>;
+      kern<<<grid, 256, 0, st>>>((const uint16_t*)x, ldx, (const void*)w, (const void*)b, (uint16_t*)y, rows, (int)D,
+                                 eps);
+    };
+    auto by_g = [&](auto pc) {
+      switch (G) {
+        case 1: launch(std::integral_constant<int, 1>{}, pc); break;
+        case 2: launch(std::integral_constant<int, 2>{}, pc); break;
+        case 3: launch(std::integral_constant<int, 3>{}, pc); break;
+        case 4: launch(std::integral_constant<int, 4>{}, pc); break;
+        case 5: launch(std::integral_constant<int, 5>{}, pc); break;
+        case 6: launch(std::integral_constant<int, 6>{}, pc); break;
+        case 7: launch(std::integral_constant<int, 7>{}, pc); break;
+        default: launch(std::integral_constant<int, 8>{}, pc); break;
+      }
+    };
+    switch (pk) {
+      case 0: by_g(std::integral_constant<int, 0>{}); break;
+      case 1: by_g(std::integral_constant<int, 1>{}); break;
+      case 2: by_g(std::integral_constant<int, 2>{}); break;
+      default: by_g(std::integral_constant<int, 3>{}); break;
     }
-#undef LN_CASE
   } else {
     layernorm_kernel<<<grid, 256, 0, st>>>(dt_x, (const void*)x, ldx, dt_w, (const void*)w, (const void*)b, dt_y,
                                            (void*)y, rows, D, eps);
