@@ -53,6 +53,17 @@ enum {
 #define HB_EPI_BIAS 1u  /* y += bias[n] (f32 add before the one rounding) */
 #define HB_EPI_RESID 2u /* y = round(round(x.w^T) + resid): linear then add, as two contract ops */
 #define HB_EPI_GEGLU 4u /* w has 2N rows; y[:, j] = gelu(round(h[:, j])) * round(h[:, N + j]) */
+#define HB_X_PANEL 8u   /* x is in panel order (below); ldx is ignored */
+#define HB_Y_PANEL 16u  /* y is written in panel order; ldy is ignored */
+
+/* Panel order of a 16-bit [M, K] matrix (K % 16 == 0), an internal layout
+ * for activations that feed a large-M linear layer: the matrix is cut into
+ * 32-row x 16-column blocks of 1 KB, block (i, j) at element offset
+ * (i * (K/16) + j) * 512; inside a block, 16-byte chunk c = 32*h + r holds
+ * row 32*i + r, columns 16*j + 8*h ... 16*j + 8*h + 7.  This is the operand
+ * order of v_mfma_f32_32x32x16 (lane l reads chunk l), so the GEMM loads one
+ * whole block per instruction instead of 32 bytes of 32 rows.  Storage holds
+ * ceil(M/32)*32 rows; rows M... of the last block are padding. */
 
 /* hb_unary ops (tensor-backend/src/index.ts:177-198, 265-300) */
 enum {
@@ -151,6 +162,11 @@ int hb_event_destroy(uintptr_t ev);
  *         columns; bias (if any) has 2N entries. */
 int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintptr_t w, uintptr_t bias, uintptr_t resid,
               int64_t ldr, uintptr_t y, int64_t ldy, int64_t M, int64_t N, int64_t K, unsigned flags);
+/*  HB_X_PANEL / HB_Y_PANEL (hb_linear and hb_qlinear): x read from / y
+ *  written in panel order.  Taken by the large-M kernel only: dt f16 or
+ *  bf16, M >= 4096, K % 64 == 0, 16-byte aligned operands; a panel-order y
+ *  also needs N % 16 == 0 and no residual.  Other calls fail.  The
+ *  arithmetic is the same as with row-major operands, bit for bit. */
 
 /* Quantized linear: y = x . dequant(W)^T (+ epilogue), W [N, K] in the
  * laya-js quantized layout v1 (HostQuantized, tensor-backend/src/index.ts:98-115;
@@ -176,6 +192,24 @@ int hb_qgather(uintptr_t ctx, uintptr_t qw, uintptr_t scales, uintptr_t zeros, i
  * two-pass statistics; w / b may be 0.  Backend.layerNorm (index.ts:216-217). */
 int hb_layernorm(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt_w, uintptr_t w, uintptr_t b, int dt_y,
                  uintptr_t y, int64_t rows, int64_t D, float eps);
+
+/* hb_layernorm with y (of x's dtype) written in panel order, for a
+ * LayerNorm whose consumer is a large-M linear layer (the encoder's
+ * attn_norm -> Wqkv and mlp_norm -> Wi, modernbert/src/index.ts:347-354).
+ * Same arithmetic as hb_layernorm's 16-bit path, bit for bit; needs dt_x
+ * f16 or bf16, D % 256 == 0, D <= 2048, ldx % 4 == 0, x 8-byte aligned and
+ * the parameters aligned for 4-wide loads (8 bytes; 16 for f32).  Padding
+ * rows of the last block are written as zeros. */
+int hb_layernorm_panel(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt_w, uintptr_t w, uintptr_t b,
+                       uintptr_t y, int64_t rows, int64_t D, float eps);
+
+/* Conversions between row-major (row stride ld) and panel order for a
+ * 16-bit [M, K] matrix, K % 16 == 0: the host materialises a row-major
+ * tensor from a panel-order one when an op other than a linear layer reads
+ * it.  Buffers must be 16-byte aligned, ld % 8 == 0; hb_panel_pack writes
+ * the padding rows as zeros. */
+int hb_panel_pack(uintptr_t ctx, uintptr_t src, int64_t ld, uintptr_t dst, int64_t M, int64_t K);
+int hb_panel_unpack(uintptr_t ctx, uintptr_t src, uintptr_t dst, int64_t ld, int64_t M, int64_t K);
 
 /* Split-half RoPE on x [B, H, L, D] addressed by element strides xs[4];
  * y is contiguous [B, H, L, D].  Angles follow the f32 rule of the CPU

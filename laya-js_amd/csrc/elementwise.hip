@@ -68,6 +68,34 @@ __global__ void copy_bytes_kernel(const uint4v* __restrict__ x, uint4v* __restri
     y[i] = x[i];
 }
 
+// Panel order <-> row-major for a 16-bit [M, K] matrix: one thread per
+// 16-byte panel chunk p = 64 * block + 32 * h + r of block (i, j) =
+// divmod(block, K / 16), i.e. row 32 * i + r, columns 16 * j + 8 * h + 0..7.
+__device__ __forceinline__ void panel_chunk_rc(int64_t p, int64_t K, int64_t& row, int64_t& col) {
+  const int64_t blk = p >> 6, kb = K >> 4;
+  const int c = (int)(p & 63);
+  row = (blk / kb) * 32 + (c & 31);
+  col = (blk % kb) * 16 + (c >> 5) * 8;
+}
+
+__global__ void panel_pack_kernel(const uint16_t* __restrict__ src, int64_t ld, uint4v* __restrict__ dst, int64_t M,
+                                  int64_t K, int64_t chunks) {
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < chunks; p += (int64_t)gridDim.x * blockDim.x) {
+    int64_t row, col;
+    panel_chunk_rc(p, K, row, col);
+    dst[p] = row < M ? *(const uint4v*)(src + row * ld + col) : uint4v{0, 0, 0, 0};
+  }
+}
+
+__global__ void panel_unpack_kernel(const uint4v* __restrict__ src, uint16_t* __restrict__ dst, int64_t ld, int64_t M,
+                                    int64_t K, int64_t chunks) {
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < chunks; p += (int64_t)gridDim.x * blockDim.x) {
+    int64_t row, col;
+    panel_chunk_rc(p, K, row, col);
+    if (row < M) *(uint4v*)(dst + row * ld + col) = src[p];
+  }
+}
+
 __global__ void fill_kernel(uint8_t* __restrict__ y, uint8_t v, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     y[i] = v;
@@ -423,6 +451,33 @@ int hb_scan(uintptr_t ctx, int op, int dt_x, uintptr_t x, int64_t outer, int64_t
   scan_kernel<<<grid_for(total, 256), 256, 0, stream_of(ctx)>>>(op, dt_x, (const void*)x, outer, n, inner, dt_y,
                                                                  (void*)y);
   check_launch("hb_scan");
+  HB_API_END
+}
+
+static void check_panel_args(const char* op, uintptr_t a, uintptr_t b, int64_t ld, int64_t M, int64_t K) {
+  if (M < 0 || K <= 0 || K % 16 != 0 || ld < K || ld % 8 != 0 || a % 16 != 0 || b % 16 != 0)
+    throw std::runtime_error(std::string(op) + ": needs K % 16 == 0, ld >= K, ld % 8 == 0 and 16-byte aligned buffers");
+}
+
+int hb_panel_pack(uintptr_t ctx, uintptr_t src, int64_t ld, uintptr_t dst, int64_t M, int64_t K) {
+  HB_API_BEGIN
+  check_panel_args("hb_panel_pack", src, dst, ld, M, K);
+  const int64_t chunks = (M + 31) / 32 * 32 * (K / 8);
+  if (chunks == 0) return 0;
+  panel_pack_kernel<<<grid_for(chunks, 256), 256, 0, stream_of(ctx)>>>((const uint16_t*)src, ld, (uint4v*)dst, M, K,
+                                                                        chunks);
+  check_launch("hb_panel_pack");
+  HB_API_END
+}
+
+int hb_panel_unpack(uintptr_t ctx, uintptr_t src, uintptr_t dst, int64_t ld, int64_t M, int64_t K) {
+  HB_API_BEGIN
+  check_panel_args("hb_panel_unpack", src, dst, ld, M, K);
+  const int64_t chunks = (M + 31) / 32 * 32 * (K / 8);
+  if (chunks == 0) return 0;
+  panel_unpack_kernel<<<grid_for(chunks, 256), 256, 0, stream_of(ctx)>>>((const uint4v*)src, (uint16_t*)dst, ld, M,
+                                                                          K, chunks);
+  check_launch("hb_panel_unpack");
   HB_API_END
 }
 

@@ -378,7 +378,7 @@ template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_mfma_arow(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W, QW qw,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
-    int64_t ldy, int M, int N, int K, int tiles_n, int tiles) {
+    int64_t ldy, int M, int N, int K, int tiles_n, int tiles, int xpan, int ypan) {
   constexpr int NT = 256, BM = 256, BK = 64;
   constexpr int TM = 2, TN = BN / 32;  // 32x32 blocks per wave
   constexpr int KS = BK / 16;          // k16 substeps per stage
@@ -414,9 +414,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto tile_m0 = [&](int i) { return (mb0 + (slot + i * nx) % mx) * BM; };
   auto tile_n0 = [&](int i) { return ((slot + i * nx) / mx) * BNO; };
 
+  // X is row-major (x[row * ldx + k]) or in panel order (xpan; 32-row x
+  // 16-column blocks of 1 KB in MFMA operand order, rows padded to a multiple
+  // of 32).  For k % 8 == 0 both are x[xs_hi * (row / 32) + xs_lo * (row % 32)
+  // + xk * k]; in panel order one fragment load then reads one whole block.
+  const int64_t xs_hi = xpan ? (int64_t)32 * K : (int64_t)32 * ldx;
+  const int64_t xs_lo = xpan ? 8 : ldx;
+  const int xk = xpan ? 32 : 1;
+  const int mlim = xpan ? ((M + 31) & ~31) : M;
   // Loads are branch-free: addresses are clamped into the operand.  Rows past
   // M (A) or N (W) only feed outputs that are never stored, so they need no
-  // zeroing; a K tail (K % 64 != 0, KTAIL) is zeroed.
+  // zeroing; a K tail (K % 64 != 0, KTAIL, row-major X only) is zeroed.
   auto load_a = [&](int m0, int k0, uint4v (&a)[TM][KS]) {
     const int arow = m0 + wave * 64 + l32;
 #pragma unroll
@@ -424,7 +432,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int s = 0; s < KS; s++) {
         const int row = arow + rb * 32, k = k0 + s * 16 + lg * 8;
-        const uint4v v = *(const uint4v*)(X + (int64_t)(row < M ? row : M - 1) * ldx + (KTAIL && k >= K ? 0 : k));
+        const int rc = row < mlim ? row : mlim - 1;
+        const uint4v v = *(const uint4v*)(X + (int64_t)(rc >> 5) * xs_hi + (int64_t)(rc & 31) * xs_lo +
+                                          (int64_t)xk * (KTAIL && k >= K ? 0 : k));
         a[rb][s] = (KTAIL && k >= K) ? uint4v{0, 0, 0, 0} : v;
       }
   };
@@ -586,10 +596,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   };
   // the C tile -> Y: thread t takes chunks t, t + 256, ...; consecutive
-  // threads cover consecutive 16-byte pieces of a row
+  // threads cover consecutive 16-byte pieces of a row (row-major Y) or of a
+  // 1 KB block (panel-order Y, ypan: chunk q is row 32 * rb + q % 32, column
+  // chunk 2 * nb + (q / 32) % 2 with (rb, nb) = divmod(q / 64, CPR / 2))
+  static_assert(CPR % 2 == 0, "panel-order output needs whole 16-column blocks");
+  const int yblk = (N + 15) >> 4;  // 16-column blocks per panel-order row block
+  auto panel_chunk = [&](int q, int& r, int& c) -> int64_t {
+    const int r32 = q & 31, h = (q >> 5) & 1, rest = q >> 6, rb = rest / (CPR / 2), nb = rest - rb * (CPR / 2);
+    r = rb * 32 + r32;
+    c = nb * 2 + h;
+    return ((int64_t)rb * yblk + nb) * 512 + (h * 32 + r32) * 8;  // relative to the tile's first block
+  };
   auto write_out = [&](int m0, int n0) {
     int t0 = tid;
     asm volatile("" : "+v"(t0));
+    if (ypan) {
+      uint16_t* yb = Y + ((int64_t)(m0 >> 5) * yblk + (n0 >> 4)) * 512;
+      const int rbl = ((M + 31) >> 5) - (m0 >> 5);  // row blocks of the padded output left from m0
+      for (int q = t0; q < BM * CPR; q += NT) {
+        int r, c;
+        const int64_t o = panel_chunk(q, r, c);
+        if ((r >> 5) >= rbl || n0 + c * 8 >= N) continue;
+        *(uint4v*)(yb + o) = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+      }
+      return;
+    }
     if (m0 + BM <= M && n0 + BNO <= N) {  // interior tile: no bounds checks
       uint16_t* yb = Y + (int64_t)m0 * ldy + n0;
 #pragma unroll
@@ -614,15 +645,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   };
 
+  // Spread write-out: in a block that streams several tiles, an interior
+  // tile's output waits in the C tile and leaves during the first
+  // WO_STAGES stages of the next tile (PER_STAGE 16-byte chunks per thread
+  // and stage) instead of in one burst that every CU issues at the same
+  // moment.  The residual DMA of the next tile then starts at stage
+  // res_stage, after the C tile has drained.
+  constexpr int WO_STAGES = 6, PER_STAGE = BM * CPR / NT / WO_STAGES;
+  static_assert(PER_STAGE * WO_STAGES * NT == BM * CPR, "write-out parts");
+  const bool spread = KT >= 2 * WO_STAGES;
+  const int res_stage = spread ? WO_STAGES : 0;
+  int wo_m0 = -1, wo_n0 = 0, it_cur = 0;  // wo_m0 < 0: no output pending
+  auto write_part = [&](int part) {
+    int t0 = tid;
+    asm volatile("" : "+v"(t0));
+    if (ypan) {
+      uint16_t* yb = Y + ((int64_t)(wo_m0 >> 5) * yblk + (wo_n0 >> 4)) * 512;
+#pragma unroll
+      for (int k = 0; k < PER_STAGE; k++) {
+        int r, c;
+        const int64_t o = panel_chunk(t0 + (part * PER_STAGE + k) * NT, r, c);
+        *(uint4v*)(yb + o) = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+      }
+      return;
+    }
+    uint16_t* yb = Y + (int64_t)wo_m0 * ldy + wo_n0;
+#pragma unroll
+    for (int k = 0; k < PER_STAGE; k++) {
+      const int q = t0 + (part * PER_STAGE + k) * NT, r = q / CPR, c = q - r * CPR;
+      *(uint4v*)(yb + (int64_t)r * ldy + c * 8) = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+    }
+  };
+
   uint4v A0[TM][KS], A1[TM][KS], A2[TM][KS];
   BRegs B0, B1;
   // step g: MFMAs on `ac` and LDS buffer g&1; loads stage g+2 of the stream
   // into (al, bl); stages the W tile of g+1 (held in bs) into the other buffer.
-  auto step = [&](int g, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl, BRegs& bs) {
-    if (R != nullptr) {  // the residual tile arrives while the tile computes
-      const int it = g / KT;
-      if (g == it * KT) dma_resid(tile_m0(it), tile_n0(it));
-    }
+  auto step = [&](int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl, BRegs& bs) {
+    // the residual tile arrives while the tile computes, once the previous
+    // tile's output has left the C tile
+    if (R != nullptr && kin == res_stage) dma_resid(tile_m0(it_cur), tile_n0(it_cur));
     const int g2 = g + 2 < S ? g + 2 : S - 1;
     const int i2 = g2 / KT, k2 = (g2 - i2 * KT) * BK;
     load_a(tile_m0(i2), k2, al);
@@ -652,6 +714,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     store_b((g + 1) & 1, bs);
     __builtin_amdgcn_sched_group_barrier(0x200, B_LD, 0);
+    // a sixth of the previous tile's output, issued after this stage's loads
+    // and after the wait for the previous stage's: the stores then only have
+    // to complete by the wait two stages on
+    if (wo_m0 >= 0 && kin < WO_STAGES) write_part(kin);
     __syncthreads();
   };
 
@@ -669,15 +735,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // only when KT % 6 == 0 (the launcher gives every block one tile otherwise).
   for (int it = 0; it < ntile; it++) {
     const int g0 = it * KT;
+    it_cur = it;
     for (int kt = 0; kt < KT; kt += 6) {
-      step(g0 + kt, A0, A2, B0, B1);
-      if (kt + 1 < KT) step(g0 + kt + 1, A1, A0, B1, B0);
-      if (kt + 2 < KT) step(g0 + kt + 2, A2, A1, B0, B1);
-      if (kt + 3 < KT) step(g0 + kt + 3, A0, A2, B1, B0);
-      if (kt + 4 < KT) step(g0 + kt + 4, A1, A0, B0, B1);
-      if (kt + 5 < KT) step(g0 + kt + 5, A2, A1, B1, B0);
+      step(g0 + kt, kt, A0, A2, B0, B1);
+      if (kt + 1 < KT) step(g0 + kt + 1, kt + 1, A1, A0, B1, B0);
+      if (kt + 2 < KT) step(g0 + kt + 2, kt + 2, A2, A1, B0, B1);
+      if (kt + 3 < KT) step(g0 + kt + 3, kt + 3, A0, A2, B1, B0);
+      if (kt + 4 < KT) step(g0 + kt + 4, kt + 4, A1, A0, B0, B1);
+      if (kt + 5 < KT) step(g0 + kt + 5, kt + 5, A2, A1, B1, B0);
+      if (kt == 0) wo_m0 = -1;  // the previous tile's output has left
     }
-    // the residual DMA of the tile's first stage has landed once at most the
+    // the residual DMA (stage res_stage < KT - 1) has landed once at most the
     // W and A loads of one stage are outstanding (they were all issued after
     // it, and loads complete in order); the barrier makes every wave's part
     // of the C tile visible (and, without R, keeps the previous tile's
@@ -704,8 +772,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
     __syncthreads();
-    write_out(tile_m0(it), tile_n0(it));
-    if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
+    const int m0 = tile_m0(it), n0 = tile_n0(it);
+    if (spread && it + 1 < ntile && m0 + BM <= M && n0 + BNO <= N) {
+      wo_m0 = m0;  // leaves during the next tile's first stages
+      wo_n0 = n0;
+    } else {
+      write_out(m0, n0);
+      if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
+    }
   }
 }
 
@@ -818,9 +892,9 @@ static void launch_mfma(hipStream_t st, const uint16_t* x, int64_t ldx, const ui
 }
 
 template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
-static void launch_arow(hipStream_t st, int cus, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
-                        const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
-                        int K) {
+static void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                        QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
+                        int N, int K) {
   constexpr int BNO = GEGLU ? BN / 2 : BN;
   const int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO, tiles = tiles_m * tiles_n;
   // one persistent block per CU, a multiple of 8 (one per XCD); with
@@ -837,33 +911,51 @@ static void launch_arow(hipStream_t st, int cus, const uint16_t* x, int64_t ldx,
     HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr = true;
   }
-  kern<<<grid, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n, tiles);
+  kern<<<grid, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n, tiles, (pan & HB_X_PANEL) ? 1 : 0,
+                               (pan & HB_Y_PANEL) ? 1 : 0);
 }
 
+// The large-M kernel runs for M >= 4096; it is the only one that takes
+// panel-order operands (the entry points check that before dispatching).
+static bool arow_path(int64_t M) { return M >= 4096; }
+
 template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
-static void mfma_dispatch(hipStream_t st, int cus, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
-                          const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
-                          int K) {
+static void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                          QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
+                          int N, int K) {
   // large M: persistent 256 x 192 tiles with register-resident A rows; otherwise 128 x 128
-  if ((int64_t)M >= 4096 && K % 64 == 0)
-    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, false>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-  else if ((int64_t)M >= 4096)
-    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  if (arow_path(M) && K % 64 == 0)
+    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, false>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  else if (arow_path(M))
+    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   else
     launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
 }
 
 template <int QB, bool AFF, bool SF32>
-static void mfma_dtype(int dt, bool geglu, hipStream_t st, int cus, const uint16_t* x, int64_t ldx, const uint16_t* w,
-                       QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
-                       int N, int K) {
+static void mfma_dtype(int dt, bool geglu, hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx,
+                       const uint16_t* w, QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y,
+                       int64_t ldy, int M, int N, int K) {
   if (dt == HB_F16) {
-    if (geglu) mfma_dispatch<false, true, QB, AFF, SF32>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-    else mfma_dispatch<false, false, QB, AFF, SF32>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    if (geglu) mfma_dispatch<false, true, QB, AFF, SF32>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    else mfma_dispatch<false, false, QB, AFF, SF32>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   } else {
-    if (geglu) mfma_dispatch<true, true, QB, AFF, SF32>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-    else mfma_dispatch<true, false, QB, AFF, SF32>(st, cus, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    if (geglu) mfma_dispatch<true, true, QB, AFF, SF32>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    else mfma_dispatch<true, false, QB, AFF, SF32>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   }
+}
+
+// Panel-order operands (HB_X_PANEL / HB_Y_PANEL) need the large-M MFMA kernel
+// with K % 64 == 0; a panel-order Y also a width of whole 16-column blocks
+// and no residual.
+static void check_panel(unsigned flags, bool mfma, int64_t M, int64_t N_out, int64_t K, bool resid, const char* op) {
+  if (!(flags & (HB_X_PANEL | HB_Y_PANEL))) return;
+  if (!mfma || !arow_path(M) || K % 64 != 0)
+    throw std::runtime_error(std::string(op) +
+                             ": panel-order operands need f16/bf16, M >= 4096, K % 64 == 0 and 16-byte aligned "
+                             "operands");
+  if ((flags & HB_Y_PANEL) && (N_out % 16 != 0 || resid))
+    throw std::runtime_error(std::string(op) + ": a panel-order y needs out % 16 == 0 and no residual");
 }
 
 static void check_linear_args(int dt, int64_t ldx, int64_t ldy, int64_t M, int64_t N, int64_t K, unsigned flags,
@@ -896,10 +988,12 @@ extern "C" int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintpt
   hipStream_t st = stream_of(ctx);
   bool mfma = (dt == HB_F16 || dt == HB_BF16) && K > 0 && K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 &&
               (!r || ldr % 8 == 0) && x % 16 == 0 && w % 16 == 0 && y % 16 == 0 && (!r || resid % 16 == 0);
+  check_panel(flags, mfma, M, N, K, r != nullptr, "hb_linear");
+  const unsigned pan = flags & (HB_X_PANEL | HB_Y_PANEL);
   if (mfma) {
     QW qw{nullptr, nullptr, nullptr, 0, 1};
-    mfma_dtype<0, false, false>(dt, geglu, st, cu_count(ctx), (const uint16_t*)x, ldx, (const uint16_t*)w, qw, (const uint16_t*)b,
-                                (const uint16_t*)r, ldr, (uint16_t*)y, ldy, (int)M, (int)N, (int)K);
+    mfma_dtype<0, false, false>(dt, geglu, st, cu_count(ctx), pan, (const uint16_t*)x, ldx, (const uint16_t*)w, qw,
+                                (const uint16_t*)b, (const uint16_t*)r, ldr, (uint16_t*)y, ldy, (int)M, (int)N, (int)K);
   } else {
     QWs qw{nullptr, nullptr, nullptr, 0, 0, 1, 0, 0};
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
@@ -934,6 +1028,8 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
   bool mfma = (dt == HB_F16 || dt == HB_BF16) && K > 0 && K % 8 == 0 && group % 8 == 0 && ldx % 8 == 0 &&
               ldy % 8 == 0 && (!r || ldr % 8 == 0) && x % 16 == 0 && y % 16 == 0 && (!r || resid % 16 == 0) &&
               qw % 8 == 0 && scales % 2 == 0 && zeros % 2 == 0;
+  check_panel(flags, mfma, M, N, K, r != nullptr, "hb_qlinear");
+  const unsigned pan = flags & (HB_X_PANEL | HB_Y_PANEL);
   if (mfma) {
     QW q{(const uint8_t*)qw, (const void*)scales, (const void*)zeros, G, group};
     const uint16_t* X = (const uint16_t*)x;
@@ -941,10 +1037,10 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
     const uint16_t* Rp = (const uint16_t*)r;
     uint16_t* Yp = (uint16_t*)y;
     int m = (int)M, n = (int)N, k = (int)K;
-    if (bits == 8 && mode == 0) mfma_dtype<8, false, false>(dt, geglu, st, cu_count(ctx), X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
-    else if (bits == 8) mfma_dtype<8, true, false>(dt, geglu, st, cu_count(ctx), X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
-    else if (mode == 0) mfma_dtype<4, false, false>(dt, geglu, st, cu_count(ctx), X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
-    else mfma_dtype<4, true, false>(dt, geglu, st, cu_count(ctx), X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    if (bits == 8 && mode == 0) mfma_dtype<8, false, false>(dt, geglu, st, cu_count(ctx), pan, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else if (bits == 8) mfma_dtype<8, true, false>(dt, geglu, st, cu_count(ctx), pan, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else if (mode == 0) mfma_dtype<4, false, false>(dt, geglu, st, cu_count(ctx), pan, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
+    else mfma_dtype<4, true, false>(dt, geglu, st, cu_count(ctx), pan, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
   } else {
     QWs q{(const uint8_t*)qw, (const void*)scales, (const void*)zeros, HB_F16, G, group, bits, mode};
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));

@@ -27,17 +27,12 @@ __device__ __forceinline__ void load4_param(const void* p, int c, float (&v)[4])
   }
 }
 
+// One row of the 16-bit path: raw[g] holds columns (g * 64 + lane) * 4 + 0..3
+// of the row; out[g] gets the normalised values at the same columns.  Both
+// 16-bit kernels below call this, so their outputs agree bit for bit.
 template <int G, bool BF, int PK>
-__global__ __launch_bounds__(256) void layernorm_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                            const void* __restrict__ w, const void* __restrict__ b,
-                                                            uint16_t* __restrict__ y, int64_t rows, int D, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const uint16_t* xr = x + row * ldx;
-  uint2v raw[G];
-#pragma unroll
-  for (int g = 0; g < G; g++) raw[g] = *(const uint2v*)(xr + (g * 64 + lane) * 4);
+__device__ __forceinline__ void ln_row(const uint2v (&raw)[G], int lane, const void* __restrict__ w,
+                                       const void* __restrict__ b, int D, float eps, uint2v (&out)[G]) {
   float v[G][4];
   float s = 0.0f;
 #pragma unroll
@@ -60,7 +55,6 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(const uint16_t* __re
       q += d * d;
     }
   const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)D + eps);
-  uint16_t* yr = y + row * (int64_t)D;
 #pragma unroll
   for (int g = 0; g < G; g++) {
     const int c = (g * 64 + lane) * 4;
@@ -79,7 +73,73 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(const uint16_t* __re
       }
       o[e] = BF ? f32_to_bf16(t) : f32_to_f16_bits(t);
     }
-    *(uint2v*)(yr + c) = uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+    out[g] = uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+  }
+}
+
+template <int G, bool BF, int PK>
+__global__ __launch_bounds__(256) void layernorm_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                            const void* __restrict__ w, const void* __restrict__ b,
+                                                            uint16_t* __restrict__ y, int64_t rows, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * ldx;
+  uint2v raw[G], out[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) raw[g] = *(const uint2v*)(xr + (g * 64 + lane) * 4);
+  ln_row<G, BF, PK>(raw, lane, w, b, D, eps, out);
+  uint16_t* yr = y + row * (int64_t)D;
+#pragma unroll
+  for (int g = 0; g < G; g++) *(uint2v*)(yr + (g * 64 + lane) * 4) = out[g];
+}
+
+// Panel-order output: a block of 256 threads normalises 8 consecutive rows
+// (2 per wave, loads issued first).  In panel order those rows' chunks of one
+// (16-column block, half) pair form one 128-byte line, so the block stages
+// its rows in LDS line by line -- chunk of row i in line l at slot
+// (i + l) % 8, which spreads a wave's writes over the banks -- and writes
+// each line whole with 8 consecutive 16-byte stores.  The grid covers the
+// padding rows of the last 32-row block, which are written as zeros.
+template <int G, bool BF, int PK>
+__global__ __launch_bounds__(256) void layernorm_panel_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                              const void* __restrict__ w, const void* __restrict__ b,
+                                                              uint16_t* __restrict__ y, int64_t rows, int D,
+                                                              float eps) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t tile[];  // [D / 8 lines][8 slots][8]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row0 = (int64_t)blockIdx.x * 8;
+  uint2v raw[2][G];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int64_t row = row0 + wave * 2 + i;
+    const uint16_t* xr = x + (row < rows ? row : rows - 1) * ldx;
+#pragma unroll
+    for (int g = 0; g < G; g++) raw[i][g] = *(const uint2v*)(xr + (g * 64 + lane) * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int r = wave * 2 + i;
+    uint2v out[G];
+    if (row0 + r < rows) {
+      ln_row<G, BF, PK>(raw[i], lane, w, b, D, eps, out);
+    } else {
+#pragma unroll
+      for (int g = 0; g < G; g++) out[g] = uint2v{0, 0};
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      const int c = (g * 64 + lane) * 4, l = c >> 3;
+      *(uint2v*)(tile + l * 64 + ((r + l) & 7) * 8 + (c & 7)) = out[g];
+    }
+  }
+  __syncthreads();
+  const int64_t kb = D >> 4;  // 16-column blocks per row
+  uint16_t* yb = y + (row0 >> 5) * kb * 512;
+  for (int q = threadIdx.x; q < D; q += 256) {
+    const int l = q >> 3, sl = q & 7, i = (sl - l) & 7;
+    const int r32 = (int)(row0 & 31) + i;
+    *(uint4v*)(yb + (int64_t)(l >> 1) * 512 + ((l & 1) * 32 + r32) * 8) = *(const uint4v*)(tile + q * 8);
   }
 }
 
@@ -130,6 +190,62 @@ __global__ void rope_kernel(int dt_x, const void* __restrict__ x, int64_t s0, in
   }
 }
 
+// Kind of the affine parameters for the 16-bit kernels: 0 none, 1 f16,
+// 2 bf16, 3 f32, -1 other.
+static int ln_param_kind(int dt_w, uintptr_t w, uintptr_t b) {
+  return (w == 0 && b == 0) ? 0 : dt_w == HB_F16 ? 1 : dt_w == HB_BF16 ? 2 : dt_w == HB_F32 ? 3 : -1;
+}
+
+// The 16-bit kernels' conditions (besides the output's).
+static bool ln_vec_ok(int dt_x, uintptr_t x, int64_t ldx, int pk, uintptr_t w, uintptr_t b, int64_t D) {
+  const int64_t pal = pk == 3 ? 16 : 8;  // parameter alignment the 4-wide loads need
+  return (dt_x == HB_F16 || dt_x == HB_BF16) && D % 256 == 0 && D <= 2048 && ldx % 4 == 0 && x % 8 == 0 && pk >= 0 &&
+         w % pal == 0 && b % pal == 0;
+}
+
+static void launch_ln16(bool panel, hipStream_t st, bool bf, int pk, const uint16_t* x, int64_t ldx, uintptr_t w,
+                        uintptr_t b, uint16_t* y, int64_t rows, int D, float eps) {
+  const int G = D / 256;
+  auto launch = [&](auto gc, auto pc) {
+    constexpr int GG = decltype(gc)::value, PP = decltype(pc)::value;
+    if (panel) {
+      constexpr size_t lds = (size_t)8 * GG * 256 * sizeof(uint16_t);  // 8 rows
+      static bool attr = false;
+      if (!attr) {
+        HB_CHECK_HIP(hipFuncSetAttribute((const void*)layernorm_panel_kernel<GG, true, PP>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        HB_CHECK_HIP(hipFuncSetAttribute((const void*)layernorm_panel_kernel<GG, false, PP>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+      }
+      auto kern = bf ? layernorm_panel_kernel<GG, true, PP> : layernorm_panel_kernel<GG, false, PP>;
+      kern<<<(unsigned)((rows + 31) / 32 * 4), 256, lds, st>>>(x, ldx, (const void*)w, (const void*)b, y, rows, D,
+                                                                eps);
+    } else {
+      auto kern = bf ? layernorm_vec_kernel<GG, true, PP> : layernorm_vec_kernel<GG, false, PP>;
+      kern<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(x, ldx, (const void*)w, (const void*)b, y, rows, D, eps);
+    }
+  };
+  auto by_g = [&](auto pc) {
+    switch (G) {
+      case 1: launch(std::integral_constant<int, 1>{}, pc); break;
+      case 2: launch(std::integral_constant<int, 2>{}, pc); break;
+      case 3: launch(std::integral_constant<int, 3>{}, pc); break;
+      case 4: launch(std::integral_constant<int, 4>{}, pc); break;
+      case 5: launch(std::integral_constant<int, 5>{}, pc); break;
+      case 6: launch(std::integral_constant<int, 6>{}, pc); break;
+      case 7: launch(std::integral_constant<int, 7>{}, pc); break;
+      default: launch(std::integral_constant<int, 8>{}, pc); break;
+    }
+  };
+  switch (pk) {
+    case 0: by_g(std::integral_constant<int, 0>{}); break;
+    case 1: by_g(std::integral_constant<int, 1>{}); break;
+    case 2: by_g(std::integral_constant<int, 2>{}); break;
+    default: by_g(std::integral_constant<int, 3>{}); break;
+  }
+}
+
 }  // namespace hb
 
 using namespace hb;
@@ -142,43 +258,28 @@ int hb_layernorm(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt_w, ui
   HB_REQUIRE(D > 0 && ldx >= D, "hb_layernorm: bad row width");
   if (rows == 0) return 0;
   hipStream_t st = stream_of(ctx);
-  unsigned grid = (unsigned)((rows + 3) / 4);
-  const int pk = (w == 0 && b == 0) ? 0 : dt_w == HB_F16 ? 1 : dt_w == HB_BF16 ? 2 : dt_w == HB_F32 ? 3 : -1;
-  const int64_t pal = pk == 3 ? 16 : 8;  // parameter alignment the 4-wide loads need
-  bool vec = (dt_x == HB_F16 || dt_x == HB_BF16) && dt_y == dt_x && D % 256 == 0 && D <= 2048 && ldx % 4 == 0 &&
-             x % 8 == 0 && y % 8 == 0 && pk >= 0 && w % pal == 0 && b % pal == 0;
-  if (vec) {
-    const int G = (int)(D / 256);
-    const bool bf = dt_x == HB_BF16;
-    auto launch = [&](auto gc, auto pc) {
-      constexpr int GG = decltype(gc)::value, PP = decltype(pc)::value;
-      auto kern = bf ? layernorm_vec_kernel<GG, true, PP> : layernorm_vec_kernel<GG, false, PP>;
-      kern<<<grid, 256, 0, st>>>((const uint16_t*)x, ldx, (const void*)w, (const void*)b, (uint16_t*)y, rows, (int)D,
-                                 eps);
-    };
-    auto by_g = [&](auto pc) {
-      switch (G) {
-        case 1: launch(std::integral_constant<int, 1>{}, pc); break;
-        case 2: launch(std::integral_constant<int, 2>{}, pc); break;
-        case 3: launch(std::integral_constant<int, 3>{}, pc); break;
-        case 4: launch(std::integral_constant<int, 4>{}, pc); break;
-        case 5: launch(std::integral_constant<int, 5>{}, pc); break;
-        case 6: launch(std::integral_constant<int, 6>{}, pc); break;
-        case 7: launch(std::integral_constant<int, 7>{}, pc); break;
-        default: launch(std::integral_constant<int, 8>{}, pc); break;
-      }
-    };
-    switch (pk) {
-      case 0: by_g(std::integral_constant<int, 0>{}); break;
-      case 1: by_g(std::integral_constant<int, 1>{}); break;
-      case 2: by_g(std::integral_constant<int, 2>{}); break;
-      default: by_g(std::integral_constant<int, 3>{}); break;
-    }
+  const int pk = ln_param_kind(dt_w, w, b);
+  if (dt_y == dt_x && ln_vec_ok(dt_x, x, ldx, pk, w, b, D) && y % 8 == 0) {
+    launch_ln16(false, st, dt_x == HB_BF16, pk, (const uint16_t*)x, ldx, w, b, (uint16_t*)y, rows, (int)D, eps);
   } else {
-    layernorm_kernel<<<grid, 256, 0, st>>>(dt_x, (const void*)x, ldx, dt_w, (const void*)w, (const void*)b, dt_y,
-                                           (void*)y, rows, D, eps);
+    layernorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(dt_x, (const void*)x, ldx, dt_w, (const void*)w,
+                                                                 (const void*)b, dt_y, (void*)y, rows, D, eps);
   }
   check_launch("hb_layernorm");
+  HB_API_END
+}
+
+int hb_layernorm_panel(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt_w, uintptr_t w, uintptr_t b,
+                       uintptr_t y, int64_t rows, int64_t D, float eps) {
+  HB_API_BEGIN
+  HB_REQUIRE(D > 0 && ldx >= D, "hb_layernorm_panel: bad row width");
+  const int pk = ln_param_kind(dt_w, w, b);
+  HB_REQUIRE(ln_vec_ok(dt_x, x, ldx, pk, w, b, D) && y % 16 == 0,
+             "hb_layernorm_panel: needs f16/bf16, D % 256 == 0, D <= 2048, ldx % 4 == 0 and aligned operands");
+  if (rows == 0) return 0;
+  launch_ln16(true, stream_of(ctx), dt_x == HB_BF16, pk, (const uint16_t*)x, ldx, w, b, (uint16_t*)y, rows, (int)D,
+              eps);
+  check_launch("hb_layernorm_panel");
   HB_API_END
 }
 

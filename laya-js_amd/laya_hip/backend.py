@@ -18,6 +18,12 @@ Design (MI355X-first, not a port of any reference backend):
 - `sdpa` writes its output physically as [B, L, H, D] and returns a
   [B, H, L, D] view of it, so the encoder's transpose + reshape back to
   [B, L, H*D] (modernbert/src/index.ts:352) is free.
+- `layerNorm` and `geglu` of a pending linear are pending too.  When their
+  first consumer is a large-M linear layer (M >= 4096, 16-bit, K % 64 == 0)
+  they are written in panel order (laya_hip.h: 32 x 16 blocks in MFMA
+  operand order), which the GEMM loads a whole block per instruction; any
+  other reader gets a row-major copy (hb_panel_unpack).  Same values, bit
+  for bit: only the addressing differs.
 - Every output is rounded once per contract op, exactly as the op-by-op
   sequence would round it (the fused GEGLU and residual epilogues round the
   linear result before applying the next op).
@@ -136,16 +142,73 @@ class HipTensor:
 
 # ------------------------------------------------------------------ pending work
 
+PANEL_MIN_M = 4096  # the large-M GEMM, the one kernel that takes panel-order operands
+
+
+def _panel_rows(M: int) -> int:
+    return (M + 31) // 32 * 32
+
+
+class _PanelRows:
+    """The value of a tensor, an [M, K] 16-bit matrix, held in panel order
+    (rows padded to a multiple of 32) in `st`, written for a large-M linear
+    layer.  Other readers get a row-major copy (HipBackend._ready)."""
+
+    def __init__(self, st, M: int, K: int):
+        self.st, self.M, self.K = st, M, K
+
+    def release(self):
+        if self.st is not None:
+            self.st.release()
+            self.st = None
+
+
+class _PendingNorm:
+    """layerNorm not yet launched (index.ts:216-217): row-major on first
+    use, or panel order when a large-M linear layer consumes it first."""
+
+    def __init__(self, be, x, weight, bias, eps: float, dt: str):
+        st, xp, rows, D, ld = be._rows(x)
+        self.refs = [st.retain()]
+        wdt = None
+        wp = bp = 0
+        if weight is not None:
+            self.refs.append(weight._st.retain())
+            wp, wdt = be._ptr(weight), weight.dtype
+        if bias is not None:
+            self.refs.append(bias._st.retain())
+            bp, wdt = be._ptr(bias), bias.dtype
+        self.args = (DT[x.dtype][0], xp, ld, DT[wdt or "f32"][0], wp, bp)
+        self.rows, self.D, self.eps, self.dt = rows, D, float(eps), dt
+        # hb_layernorm_panel's conditions
+        pal = 16 if wdt == "f32" else 8
+        self.panel_ok = (x.dtype in ("f16", "bf16") and dt == x.dtype and D % 256 == 0 and D <= 2048 and
+                         ld % 4 == 0 and xp % 8 == 0 and wdt in (None, "f16", "bf16", "f32") and wp % pal == 0 and
+                         bp % pal == 0)
+
+    def release(self):
+        for s in self.refs:
+            s.release()
+        self.refs = []
+
+
 class _PendingLinear:
     """y = x . w^T (+bias) not yet launched.  Captures device addresses and
     holds a reference on every operand's storage, so the caller may dispose
-    the operand tensors before the launch."""
+    the operand tensors before the launch.  `epi` is HB_EPI_GEGLU once a
+    geglu has absorbed it; `panel` (a _PanelRows) when x is in panel order."""
 
-    def __init__(self, be, x, w, bias, q=None):
+    def __init__(self, be, x, w, bias, q=None, panel=None):
         self.be = be
-        st, xp, M, K, ldx = be._rows(x)
-        self.x = (xp, M, K, ldx)
-        self.refs = [st.retain(), w._st.retain()]
+        self.epi = 0
+        self.panel = panel
+        if panel is not None:
+            self.x = (panel.st.ptr, panel.M, panel.K, panel.K)
+            self.refs = [panel.st.retain(), w._st.retain()]
+        else:
+            st, xp, M, K, ldx = be._rows(x)
+            self.x = (xp, M, K, ldx)
+            self.refs = [st.retain(), w._st.retain()]
         self.wp = be._ptr(w)
         self.bp = 0
         if bias is not None:
@@ -162,6 +225,29 @@ class _PendingLinear:
             self.q = (be._ptr(scales), zp, bits, group, 1 if mode == "affine" else 0)
         self.N = w.shape[0] if q is None else q[5]
         self.dtype = x.dtype
+        M, K = self.x[1], self.x[2]
+        # the large-M MFMA kernel takes this launch (panel-order operands
+        # allowed): hb_linear / hb_qlinear's conditions on everything but the
+        # output and the residual, which are checked at launch
+        ok = x.dtype in ("f16", "bf16") and M >= PANEL_MIN_M and K % 64 == 0 and self.x[0] % 16 == 0
+        if q is None:
+            ok = ok and self.wp % 16 == 0
+        else:
+            sp, zp, bits, group, mode = self.q
+            ok = ok and self.wp % 8 == 0 and sp % 2 == 0 and zp % 2 == 0 and group % 8 == 0
+        self.arow_ok = ok
+
+    def fork(self, epi: int) -> "_PendingLinear":
+        """The same product with epilogue `epi` (own references)."""
+        c = object.__new__(_PendingLinear)
+        c.__dict__.update(self.__dict__)
+        c.refs = [s.retain() for s in self.refs]
+        c.epi = epi
+        return c
+
+    @property
+    def n_out(self) -> int:
+        return self.N // 2 if self.epi & F.HB_EPI_GEGLU else self.N
 
     def release(self):
         for s in self.refs:
@@ -171,19 +257,33 @@ class _PendingLinear:
     def launch(self, y_ptr: int, ldy: int, flags: int = 0, resid=(0, 0)):
         be = self.be
         xp, M, K, ldx = self.x
+        flags |= self.epi
         if self.bp:
             flags |= F.HB_EPI_BIAS
         if resid[0]:
             flags |= F.HB_EPI_RESID
+        tmp = None
+        if self.panel is not None:
+            if resid[0] and (resid[0] % 16 or resid[1] % 8):
+                # a residual the large-M kernel cannot read: unpack x first
+                tmp = be._malloc(M * K * 2)
+                be._call("linear", "hb_panel_unpack", be.ctx, xp, tmp.ptr, K, M, K)
+                xp, ldx = tmp.ptr, K
+            else:
+                flags |= F.HB_X_PANEL
         N = self.N // 2 if flags & F.HB_EPI_GEGLU else self.N
         dt = DT[self.dtype][0]
-        if self.q is None:
-            be._call("linear", "hb_linear", be.ctx, dt, xp, ldx, self.wp, self.bp, resid[0], resid[1], y_ptr,
-                     ldy, M, N, K, flags)
-        else:
-            sp, zp, bits, group, mode = self.q
-            be._call("quantizedLinear", "hb_qlinear", be.ctx, dt, xp, ldx, self.wp, sp, zp, self.bp, resid[0],
-                     resid[1], y_ptr, ldy, M, N, K, bits, group, mode, flags)
+        try:
+            if self.q is None:
+                be._call("linear", "hb_linear", be.ctx, dt, xp, ldx, self.wp, self.bp, resid[0], resid[1], y_ptr,
+                         ldy, M, N, K, flags)
+            else:
+                sp, zp, bits, group, mode = self.q
+                be._call("quantizedLinear", "hb_qlinear", be.ctx, dt, xp, ldx, self.wp, sp, zp, self.bp, resid[0],
+                         resid[1], y_ptr, ldy, M, N, K, bits, group, mode, flags)
+        finally:
+            if tmp is not None:
+                tmp.release()
 
 
 class _PendingRope:
@@ -218,12 +318,12 @@ class HipBackend:
         self._prof_only = self._LAUNCHES
         self._event_pool: list[int] = []
         self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "sdpa": 0,
-                      "sdpa_fused_rope": 0, "copies": 0}
+                      "sdpa_fused_rope": 0, "copies": 0, "panel_unpacks": 0}
 
     # ---------------------------------------------------------------- plumbing
     # kernel-launching entry points (timed per op key while profiling)
-    _LAUNCHES = frozenset(("hb_linear", "hb_qlinear", "hb_qgather", "hb_layernorm", "hb_rope", "hb_sdpa",
-                           "hb_sdpa_mask_info", "hb_geglu",
+    _LAUNCHES = frozenset(("hb_linear", "hb_qlinear", "hb_qgather", "hb_layernorm", "hb_layernorm_panel",
+                           "hb_panel_unpack", "hb_panel_pack", "hb_rope", "hb_sdpa", "hb_sdpa_mask_info", "hb_geglu",
                            "hb_unary", "hb_binary", "hb_where", "hb_gather", "hb_reduce", "hb_scan", "hb_meanpool"))
 
     def _call(self, op: str, name: str, *args):
@@ -316,7 +416,21 @@ class HipBackend:
             st = self._malloc(_numel(t.shape) * DT[t.dtype][1])
             t._st, t._off, t._strides = st, 0, _contig(t.shape)
             self.stats["linear"] += 1
-            lz.launch(st.ptr, lz.N)
+            lz.launch(st.ptr, lz.n_out)
+            lz.release()
+        elif isinstance(lz, _PendingNorm):
+            st = self._malloc(_numel(t.shape) * DT[t.dtype][1])
+            t._st, t._off, t._strides = st, 0, _contig(t.shape)
+            dtx, xp, ld, dtw, wp, bp = lz.args
+            if lz.rows:
+                self._call("layerNorm", "hb_layernorm", self.ctx, dtx, xp, ld, dtw, wp, bp, DT[lz.dt][0], st.ptr,
+                           lz.rows, lz.D, lz.eps)
+            lz.release()
+        elif isinstance(lz, _PanelRows):
+            st = self._malloc(_numel(t.shape) * DT[t.dtype][1])
+            t._st, t._off, t._strides = st, 0, _contig(t.shape)
+            self.stats["panel_unpacks"] += 1
+            self._call("read", "hb_panel_unpack", self.ctx, lz.st.ptr, st.ptr, lz.K, lz.M, lz.K)
             lz.release()
         elif isinstance(lz, _PendingRope):
             src_st, off, strides, dtype, shape = lz.src
@@ -328,6 +442,31 @@ class HipBackend:
                        DT[t.dtype][0], st.ptr, B, H, L, D, lz.base)
             lz.release()
         return t
+
+    def _as_panel(self, x: HipTensor) -> Optional[_PanelRows]:
+        """x's value in panel order for a large-M linear layer: already there,
+        or written so now if x is a pending layerNorm or a pending GeGLU
+        linear that can write it; else None."""
+        lz = x._lazy
+        if isinstance(lz, _PanelRows):
+            return lz
+        if isinstance(lz, _PendingNorm) and lz.panel_ok and lz.rows >= PANEL_MIN_M and lz.D % 64 == 0:
+            st = self._malloc(_panel_rows(lz.rows) * lz.D * 2)
+            dtx, xp, ld, dtw, wp, bp = lz.args
+            self._call("layerNorm", "hb_layernorm_panel", self.ctx, dtx, xp, ld, dtw, wp, bp, st.ptr, lz.rows, lz.D,
+                       lz.eps)
+            lz.release()
+            x._lazy = _PanelRows(st, lz.rows, lz.D)
+            return x._lazy
+        if (isinstance(lz, _PendingLinear) and lz.epi == F.HB_EPI_GEGLU and lz.arow_ok and lz.n_out % 64 == 0):
+            M = lz.x[1]
+            st = self._malloc(_panel_rows(M) * lz.n_out * 2)
+            self.stats["linear"] += 1
+            lz.launch(st.ptr, lz.n_out, F.HB_Y_PANEL)
+            lz.release()
+            x._lazy = _PanelRows(st, M, lz.n_out)
+            return x._lazy
+        return None
 
     def _ptr(self, t: HipTensor) -> int:
         self._ready(t)
@@ -699,7 +838,9 @@ class HipBackend:
 
     def _try_fuse_resid(self, r: HipTensor, lin: HipTensor) -> Optional[HipTensor]:
         lz = lin._lazy
-        if not isinstance(lz, _PendingLinear) or r._lazy is not None:
+        if not isinstance(lz, _PendingLinear) or lz.epi:
+            return None
+        if r._lazy is not None and not isinstance(r._lazy, (_PanelRows, _PendingNorm)):
             return None
         if r.shape != lin.shape or r.dtype != lin.dtype:
             return None
@@ -931,8 +1072,25 @@ class HipBackend:
             if b.shape != (w.shape[0],):
                 raise ValueError(f"linear: bias [{','.join(map(str, b.shape))}] vs out {w.shape[0]}")
             b = self._contiguous(b if b.dtype == dt else self.cast(b, dt))
-        pend = _PendingLinear(self, x, w, b)
+        pend = _PendingLinear(self, x, w, b, panel=self._panel_for(x, w=w))
         return self._track(HipTensor(x.shape[:-1] + (w.shape[0],), dt, None, lazy=pend))
+
+    def _panel_for(self, x: HipTensor, w: Optional[HipTensor] = None, q=None) -> Optional[_PanelRows]:
+        """The panel-order form of x when this linear layer takes the large-M
+        kernel (weights side checked here, x side by _as_panel)."""
+        if x.dtype not in ("f16", "bf16") or not x.shape or _numel(x.shape[:-1]) < PANEL_MIN_M:
+            return None
+        if x._lazy is None or isinstance(x._lazy, _PendingRope):
+            return None
+        if q is None:
+            if self._ptr(w) % 16:
+                return None
+        else:
+            qw, scales, zeros, group = q
+            if (self._ptr(qw) % 8 or self._ptr(scales) % 2 or (zeros is not None and self._ptr(zeros) % 2)
+                    or group % 8):
+                return None
+        return self._as_panel(x)
 
     def layerNorm(self, x: HipTensor, weight: Optional[HipTensor], bias: Optional[HipTensor], eps: float):
         self._live(x, weight, bias, op="layerNorm")
@@ -948,11 +1106,8 @@ class HipBackend:
             if wdt is not None and bias.dtype != wdt:
                 bias = self.cast(bias, wdt)
             bp, wdt = self._ptr(bias), bias.dtype
-        out = self._new(x.shape, dt)
-        if rows:
-            self._call("layerNorm", "hb_layernorm", self.ctx, DT[x.dtype][0], xp, ld, DT[wdt or "f32"][0], wp, bp,
-                       DT[dt][0], out._st.ptr, rows, D, float(eps))
-        return out
+        pend = _PendingNorm(self, x, weight, bias, eps, dt)
+        return self._track(HipTensor(x.shape, dt, None, lazy=pend))
 
     def embedding(self, table: HipTensor, ids: HipTensor) -> HipTensor:
         self._live(table, ids, op="embedding")
@@ -1073,11 +1228,9 @@ class HipBackend:
         if F2 % 2:
             raise ValueError("geglu: last axis must be even")
         lz = x._lazy
-        if isinstance(lz, _PendingLinear):
-            out = self._new(x.shape[:-1] + (F2 // 2,), x.dtype)
+        if isinstance(lz, _PendingLinear) and lz.epi == 0:
             self.stats["linear_fused_geglu"] += 1
-            lz.launch(out._st.ptr, F2 // 2, F.HB_EPI_GEGLU)
-            return out
+            return self._track(HipTensor(x.shape[:-1] + (F2 // 2,), x.dtype, None, lazy=lz.fork(F.HB_EPI_GEGLU)))
         dt = x.dtype if x.dtype in FLOAT_DT else "f32"
         st, xp, rows, _, ld = self._rows(x)
         out = self._new(x.shape[:-1] + (F2 // 2,), dt)
@@ -1136,7 +1289,8 @@ class HipBackend:
             x = self.cast(x, dt)
         if bias is not None:
             bias = self._contiguous(bias if bias.dtype == dt else self.cast(bias, dt))
-        pend = _PendingLinear(self, x, w, bias, (scales, biases, opts.bits, opts.groupSize, opts.mode, N))
+        pan = self._panel_for(x, q=(w, scales, biases, opts.groupSize))
+        pend = _PendingLinear(self, x, w, bias, (scales, biases, opts.bits, opts.groupSize, opts.mode, N), panel=pan)
         return self._track(HipTensor(x.shape[:-1] + (N,), dt, None, lazy=pend))
 
     def quantizedEmbedding(self, w: HipTensor, scales: HipTensor, biases: Optional[HipTensor], opts,

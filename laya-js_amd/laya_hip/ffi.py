@@ -24,6 +24,7 @@ PU64 = C.POINTER(C.c_uint64)
 # dtype codes (laya_hip.h)
 HB_F32, HB_F16, HB_BF16, HB_I32, HB_BOOL, HB_U8, HB_I8, HB_U16, HB_I16, HB_U32 = range(10)
 HB_EPI_BIAS, HB_EPI_RESID, HB_EPI_GEGLU = 1, 2, 4
+HB_X_PANEL, HB_Y_PANEL = 8, 16  # panel-order x / y (laya_hip.h)
 (HB_UN_COPY, HB_UN_SCALE, HB_UN_EXP, HB_UN_LOG, HB_UN_RELU, HB_UN_GELU, HB_UN_NEG, HB_UN_ABS, HB_UN_SQRT,
  HB_UN_RSQRT, HB_UN_TANH, HB_UN_SIGMOID, HB_UN_ERF, HB_UN_NOT) = range(14)
 (HB_BIN_ADD, HB_BIN_SUB, HB_BIN_MUL, HB_BIN_DIV, HB_BIN_MAX, HB_BIN_MIN, HB_BIN_POW, HB_BIN_EQ, HB_BIN_NE,
@@ -55,6 +56,9 @@ SYMBOLS: dict[str, tuple] = {
     "hb_qlinear": (I, [U, I, U, I64, U, U, U, U, U, I64, U, I64, I64, I64, I64, I, I, I, C.c_uint]),
     "hb_qgather": (I, [U, U, U, U, I64, I64, I, I, I, U, I64, I, U]),
     "hb_layernorm": (I, [U, I, U, I64, I, U, U, I, U, I64, I64, F]),
+    "hb_layernorm_panel": (I, [U, I, U, I64, I, U, U, U, I64, I64, F]),
+    "hb_panel_pack": (I, [U, U, I64, U, I64, I64]),
+    "hb_panel_unpack": (I, [U, U, U, I64, I64, I64]),
     "hb_rope": (I, [U, I, U, PI64, I, U, I64, I64, I64, I64, D]),
     "hb_sdpa": (I, [U, I, U, PI64, U, PI64, U, PI64, U, PI64, U, U, PI64, I64, I64, I64, I64, I64, F, D, D]),
     "hb_sdpa_mask_info_bytes": (I, [I64, I64, I64, C.POINTER(C.c_size_t)]),

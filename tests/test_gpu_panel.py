@@ -1,0 +1,168 @@
+"""Panel-order activations (laya_hip.h, HB_X_PANEL / HB_Y_PANEL): the layout,
+and bit identity of every panel-order path with its row-major twin.
+
+The encoder writes a LayerNorm output and the fused GeGLU output in panel
+order when a large-M linear layer consumes them (M >= 4096), so the GEMM
+reads one 1 KB block per load.  Only the addressing changes: the LayerNorm,
+the GEMM and its epilogues must give the same bits as with row-major
+operands, for f16 and bf16, plain, GeGLU, residual and quantized weights,
+with ragged M (padding rows in the last block, partial 256-row tiles).
+The values themselves are checked against the oracle by the linear and
+encoder tests; the batch-independence test of the encoder compares a B = 32
+forward (panel order) with B = 1 (row-major) bit for bit."""
+import numpy as np
+import pytest
+
+from gpu_util import read32, rounded, to_host
+from laya_hip import ffi as F
+from laya_hip.backend import _PanelRows
+from laya_hip.host import HostQuantized, HostTensor, pack_quantized
+from oracle import cpu_ref as cr
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def b():
+    from laya_hip.backend import HipBackend
+    be = HipBackend(0)
+    yield be
+    be.destroy()
+
+
+def _bits(b, t) -> np.ndarray:
+    return np.asarray(b.read(t).data).view(np.uint16)
+
+
+def _panel_ref(a: np.ndarray) -> np.ndarray:
+    """The documented layout: block (i, j) of 32 x 16 at (i * K/16 + j) * 512,
+    chunk 32*h + r = row 32i + r, columns 16j + 8h .. +7; padding rows 0."""
+    M, K = a.shape
+    Mp = (M + 31) // 32 * 32
+    p = np.zeros((Mp, K), a.dtype)
+    p[:M] = a
+    return p.reshape(Mp // 32, 32, K // 16, 2, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
+
+
+@pytest.mark.parametrize("M,K", [(100, 48), (4100, 768), (32, 16)])
+def test_pack_unpack_layout(b, M, K):
+    rng = np.random.default_rng(M)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    X = b.fromHost(HostTensor("f16", (M, K), a))
+    Mp = (M + 31) // 32 * 32
+    P = b._new((Mp * K,), "f16")
+    b._call("pack", "hb_panel_pack", b.ctx, b._ptr(X), K, P._st.ptr, M, K)
+    np.testing.assert_array_equal(_bits(b, P), _panel_ref(a).view(np.uint16))
+    Y = b._new((M, K), "f16")
+    b._call("unpack", "hb_panel_unpack", b.ctx, P._st.ptr, Y._st.ptr, K, M, K)
+    np.testing.assert_array_equal(_bits(b, Y), a.view(np.uint16))
+    for t in (X, P, Y):
+        b.dispose(t)
+
+
+def test_panel_entry_points_reject_unsupported_calls(b):
+    X = b.fromHost(HostTensor("f16", (64, 40), np.zeros((64, 40), np.float16)))
+    P = b._new((64 * 48,), "f16")
+    with pytest.raises(RuntimeError, match="K % 16"):
+        b._call("pack", "hb_panel_pack", b.ctx, b._ptr(X), 40, P._st.ptr, 64, 40)
+    W = b.fromHost(HostTensor("f16", (64, 40), np.zeros((64, 40), np.float16)))
+    Y = b._new((64, 64), "f16")
+    # panel-order operands only on the large-M kernel (checked before any launch)
+    with pytest.raises(RuntimeError, match="panel-order operands need"):
+        b._call("linear", "hb_linear", b.ctx, F.HB_F16, b._ptr(X), 40, b._ptr(W), 0, 0, 0, Y._st.ptr, 64, 64, 64,
+                40, F.HB_X_PANEL)
+    for t in (X, P, W, Y):
+        b.dispose(t)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("pdt", [None, "same", "f32"])
+def test_layernorm_panel_bits(b, dtype, pdt):
+    M, D = 4100, 768
+    rng = np.random.default_rng(3)
+    x = rounded(rng.standard_normal((M, D)) * 2 + 0.5, dtype)
+    X = b.fromHost(to_host(x, dtype))
+    Wt = Bt = None
+    if pdt is not None:
+        wd = dtype if pdt == "same" else "f32"
+        Wt = b.fromHost(to_host(rounded(1 + 0.1 * rng.standard_normal(D), wd), wd))
+        Bt = b.fromHost(to_host(rounded(0.1 * rng.standard_normal(D), wd), wd))
+    ref = _bits(b, b._ready(b.layerNorm(X, Wt, Bt, 1e-5)))
+    h = b.layerNorm(X, Wt, Bt, 1e-5)
+    pan = b._as_panel(h)
+    assert isinstance(pan, _PanelRows)
+    raw = np.empty(((M + 31) // 32 * 32) * D, np.uint16)
+    b._call("read", "hb_download", b.ctx, raw.ctypes.data, pan.st.ptr, raw.nbytes)
+    want = _panel_ref(ref.reshape(M, D))
+    np.testing.assert_array_equal(raw, want)  # padding rows are zeros
+    np.testing.assert_array_equal(_bits(b, h), ref)  # unpacked on read
+    assert b.stats["panel_unpacks"] > 0
+
+
+def _chain(b, X, g, Wqkv, Wi, Wo, R, dtype, materialize):
+    """LN -> Wqkv; LN -> Wi + GeGLU -> Wo + residual, as in one encoder layer."""
+    def ln():
+        h = b.layerNorm(X, g, None, 1e-5)
+        return b._ready(h) if materialize else h
+    h1 = ln()
+    qkv = b.linear(h1, Wqkv)
+    if not materialize:
+        assert isinstance(h1._lazy, _PanelRows)
+    m = b.geglu(b.linear(ln(), Wi))
+    if materialize:
+        m = b._ready(m)
+    out = b.add(R, b.linear(m, Wo))
+    if not materialize:
+        assert isinstance(m._lazy, _PanelRows)
+    return _bits(b, qkv), _bits(b, out)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("M", [4160, 8192])
+def test_panel_gemm_chain_bits(b, dtype, M):
+    H, I = 768, 1152
+    rng = np.random.default_rng(M + (dtype == "bf16"))
+    up = lambda a: b.fromHost(to_host(rounded(a, dtype), dtype))  # noqa: E731
+    X = up(rng.standard_normal((M, H)))
+    g = up(1 + 0.1 * rng.standard_normal(H))
+    Wqkv, Wi, Wo = up(rng.normal(0, 0.02, (3 * H, H))), up(rng.normal(0, 0.02, (2 * I, H))), \
+        up(rng.normal(0, 0.02, (H, I)))
+    R = up(rng.standard_normal((M, H)))
+    print(f"panel chain {dtype} M={M}", flush=True)
+    fused = _chain(b, X, g, Wqkv, Wi, Wo, R, dtype, materialize=False)
+    plain = _chain(b, X, g, Wqkv, Wi, Wo, R, dtype, materialize=True)
+    np.testing.assert_array_equal(fused[0], plain[0])
+    np.testing.assert_array_equal(fused[1], plain[1])
+    # and the values: rows of the chain against the oracle (f16 / bf16 rounding at every op)
+    rows = np.sort(rng.choice(M, 64, replace=False))
+    x32 = read32(b, X)[rows]
+    w32 = lambda t: read32(b, t)  # noqa: E731
+    h = rounded(cr.layer_norm(x32, w32(g), None, 1e-5), dtype)
+    qkv = rounded(cr.linear(h, w32(Wqkv)), dtype)
+    got = fused[0].reshape(M, 3 * H)[rows]
+    got = got.view(np.float16).astype(np.float32) if dtype == "f16" else \
+        (got.astype(np.uint32) << 16).view(np.float32)
+    assert np.max(np.abs(got - qkv)) / np.max(np.abs(qkv)) <= (2e-3 if dtype == "f16" else 8e-3)
+    for t in (X, g, Wqkv, Wi, Wo, R):
+        b.dispose(t)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_panel_quantized_bits(b, bits):
+    from laya_hip import compose as C
+    M, H, N = 4160, 768, 2304
+    rng = np.random.default_rng(bits)
+    w = rounded(rng.normal(0, 0.02, (N, H)), "f16")
+    q, s, z = cr.quantize_matrix(w, N, H, bits, 64, refine=bits == 4)
+    h = HostQuantized((N, H), bits, 64, "symmetric" if bits == 8 else "affine", pack_quantized(q, bits),
+                      HostTensor("f16", s.shape, s.view(np.float16)),
+                      HostTensor("f16", z.shape, z.view(np.float16)) if z is not None else None)
+    Q = C.upload_quantized(b, h, "f16")
+    X = b.fromHost(to_host(rounded(rng.standard_normal((M, H)), "f16"), "f16"))
+    hp = b.layerNorm(X, None, None, 1e-5)
+    y_pan = C.quantized_linear(b, hp, Q)
+    assert isinstance(hp._lazy, _PanelRows)
+    y_row = C.quantized_linear(b, b._ready(b.layerNorm(X, None, None, 1e-5)), Q)
+    np.testing.assert_array_equal(_bits(b, y_pan), _bits(b, y_row))
+    C.dispose_quantized(b, Q)
+    b.dispose(X)
