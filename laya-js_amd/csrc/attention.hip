@@ -36,6 +36,9 @@ static S4 s4(const int64_t* p) {
 }
 
 constexpr int kBQ = 128;  // queries per block
+constexpr int kQB = 1;    // 16-query blocks per wave
+constexpr int kNW = kBQ / (16 * kQB);  // waves per block
+constexpr int kNT = kNW * 64;          // threads per block
 constexpr int kBK = 64;   // keys per tile
 constexpr int kMaxKeyTiles = 1024;  // Lk <= 65536 on the MFMA path
 
@@ -119,8 +122,28 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   }
 }
 
+// 4 mask bytes (any nonzero byte is true) -> 4 bits, byte i -> bit i.
+__device__ __forceinline__ uint32_t mask_bits(uint32_t w) {
+  // bit 7 of each byte set iff the byte is nonzero (no carries between bytes)
+  const uint32_t nz = (((w & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w) & 0x80808080u;
+  // bytes' bit 0 (nz >> 7) gathered into bits 24..27 by one multiply
+  return ((nz >> 7) * 0x01020408u) >> 24;
+}
+
 __device__ __forceinline__ int qk_swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+// K tiles: chunk c of row r at c ^ (4 * bit 1 of r + bits 3..4 of r).  A
+// 16-lane pass of the S = K.Q^T fragment reads touches rows b + 8a (a, b in
+// 0..3), which this spreads over all 64 banks, and the staging stores (rows
+// r..r+3, chunks 0..3 or 4..7) hit disjoint banks too.
+__device__ __forceinline__ int k_swz(int r, int c) { return r * 64 + ((c ^ ((((r >> 1) & 1) << 2) | ((r >> 3) & 3))) << 3); }
 constexpr int kVtLd = 72;  // row stride (elements) of V^T in LDS
+// V^T tiles: the 8-key chunk c of row d sits at c ^ (4 * bit 4 of d + 2 * bit 5
+// of d), which makes the transposing staging stores (rows 8*vc + i, one
+// 32-bit key pair per lane) hit 64 distinct banks; the fragment reads of one
+// instruction share bits 4..5 of d, so they stay conflict-free.
+__device__ __forceinline__ int vt_swz(int d, int c) {
+  return d * kVtLd + ((c ^ ((((d >> 4) & 1) << 2) | (((d >> 5) & 1) << 1))) << 3);
+}
 
 // Raw chunks c and c + 4 (d in [8c, 8c+8) and the rotation partners d + 32)
 // of one row of a [L, 64] operand; zero when the row is out of range.
@@ -149,7 +172,7 @@ __device__ __forceinline__ void load_cs(const float2* __restrict__ tab, int pos,
 // Rotates a loaded chunk pair by RoPE (when `rot`) with the pairs' cos / sin,
 // rounding to the storage type like a separate Backend.rope, and writes it
 // to the swizzled [rows][64] LDS tile.
-template <bool BF16>
+template <bool BF16, bool KSWZ = false>
 __device__ __forceinline__ void store_pair(uint4v lo, uint4v hi, bool rot, int c, const float2 (&cs)[8],
                                            uint16_t* lds, int row) {
   if (rot) {
@@ -160,28 +183,25 @@ __device__ __forceinline__ void store_pair(uint4v lo, uint4v hi, bool rot, int c
       const float2 c0 = cs[2 * e], c1 = cs[2 * e + 1];
       float x0a = tof<BF16>(l[e] & 0xffff), x0b = tof<BF16>(l[e] >> 16);
       float x1a = tof<BF16>(h[e] & 0xffff), x1b = tof<BF16>(h[e] >> 16);
-      uint32_t oa = fromf<BF16>(pin_f32(fmaf(-x1a, c0.y, x0a * c0.x)));
-      uint32_t ob = fromf<BF16>(pin_f32(fmaf(-x1b, c1.y, x0b * c1.x)));
-      uint32_t pa = fromf<BF16>(pin_f32(fmaf(x0a, c0.y, x1a * c0.x)));
-      uint32_t pb = fromf<BF16>(pin_f32(fmaf(x0b, c1.y, x1b * c1.x)));
-      l[e] = oa | (ob << 16);
-      h[e] = pa | (pb << 16);
+      l[e] = pack2<BF16>(pin_f32(fmaf(-x1a, c0.y, x0a * c0.x)), pin_f32(fmaf(-x1b, c1.y, x0b * c1.x)));
+      h[e] = pack2<BF16>(pin_f32(fmaf(x0a, c0.y, x1a * c0.x)), pin_f32(fmaf(x0b, c1.y, x1b * c1.x)));
     }
   }
-  *(uint4v*)(lds + qk_swz(row, c)) = lo;
-  *(uint4v*)(lds + qk_swz(row, c + 4)) = hi;
+  *(uint4v*)(lds + (KSWZ ? k_swz(row, c) : qk_swz(row, c))) = lo;
+  *(uint4v*)(lds + (KSWZ ? k_swz(row, c + 4) : qk_swz(row, c + 4))) = hi;
 }
 
 template <bool BF16>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void sdpa_mfma(const uint16_t* __restrict__ Q, S4 qs, const uint16_t* __restrict__ K,
+__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void sdpa_mfma(const uint16_t* __restrict__ Q, S4 qs, const uint16_t* __restrict__ K,
                                                  S4 ks, const uint16_t* __restrict__ V, S4 vs,
                                                  const uint8_t* __restrict__ mask, S4 ms, int mask_vec,
                                                  const uint8_t* __restrict__ cls, uint16_t* __restrict__ O, S4 os,
                                                  int Lq, int Lk, float scale_log2, const float2* __restrict__ tabq,
                                                  const float2* __restrict__ tabk) {
+  // Q, and two buffers of K and V^T: tile t + 1 is staged while tile t computes
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBK * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[64 * kVtLd];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64 * kVtLd];
   __shared__ uint8_t cls_row[kMaxKeyTiles];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -192,9 +212,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
   const uint16_t* Qb = Q + b * qs.s[0] + h * qs.s[1];
   const uint16_t* Kb = K + b * ks.s[0] + h * ks.s[1];
   const uint16_t* Vb = V + b * vs.s[0] + h * vs.s[1];
+  // this block's Q rows (and their RoPE cos / sin) are requested first: they
+  // do not depend on the tile classes, so their latency overlaps the class
+  // row's
+  constexpr int QR = kBQ * 4 / kNT;  // rounds of Q staging (4 threads per row)
+  static_assert(QR * kNT == kBQ * 4, "Q staging: whole rounds");
+  uint4v qlo[QR], qhi[QR];
+  float2 qcs[QR][8];
+#pragma unroll
+  for (int u = 0; u < QR; u++) {
+    const int t = tid + u * kNT, r = t >> 2, c = t & 3, q = q0 + r;
+    load_pair(Qb + (int64_t)q * qs.s[2], q < Lq, c, qlo[u], qhi[u]);
+    if (tabq != nullptr && q < Lq) load_cs(tabq, q, c, qcs[u]);
+  }
+
   // tile classes of this (b, query tile): 0 skip, 1 all visible, 2 per-element
   // mask / key bound; staged in LDS once (the host caps nkt at kMaxKeyTiles)
-  for (int t = tid; t < nkt; t += 256) {
+  for (int t = tid; t < nkt; t += kNT) {
     uint8_t c;
     if (cls != nullptr) c = cls[((int64_t)b * nqt + qt) * nkt + t];
     else if (mask != nullptr) c = 2;
@@ -209,29 +243,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
   };
   __syncthreads();  // the class row is complete
 
-  // this thread's share of a K tile (row kr, chunk pair kc) and V tile
-  // (key pair vj, chunk vc), prefetched into registers one tile ahead
-  const int kr = tid >> 2, kc = tid & 3;
-  const int vc = tid & 7, vj = 2 * (tid >> 3);
-  uint4v klo, khi, va, vb;
-  float2 kcs[8];  // RoPE cos / sin of this thread's K row (fused RoPE)
+  // A K tile is staged by the first 256 threads (row kr, chunk pair kc),
+  // the V tile by the other 256 (key pair vj, chunk vc); loaded into
+  // registers two tiles ahead and staged into LDS one tile ahead
+  static_assert(kNT == 512, "K / V staging: 256 threads each");
+  const bool kpart = tid < 256;  // whole waves
+  const int kr = (tid & 255) >> 2, kc = tid & 3;
+  const int vc = tid & 7, vj = 2 * ((tid & 255) >> 3);
+  uint4v pr0, pr1;  // K threads: chunks kc and kc + 4 of row kr; V threads: keys vj and vj + 1
+  float2 kcs[8];    // RoPE cos / sin of this thread's K row (fused RoPE)
   auto prefetch = [&](int kt) {
     const int k0 = kt * kBK;
-    load_pair(Kb + (int64_t)(k0 + kr) * ks.s[2], k0 + kr < Lk, kc, klo, khi);
-    if (tabk != nullptr && k0 + kr < Lk) load_cs(tabk, k0 + kr, kc, kcs);
-    va = uint4v{0, 0, 0, 0};
-    vb = uint4v{0, 0, 0, 0};
-    if (k0 + vj < Lk) va = *(const uint4v*)(Vb + (int64_t)(k0 + vj) * vs.s[2] + vc * 8);
-    if (k0 + vj + 1 < Lk) vb = *(const uint4v*)(Vb + (int64_t)(k0 + vj + 1) * vs.s[2] + vc * 8);
+    if (kpart) {
+      load_pair(Kb + (int64_t)(k0 + kr) * ks.s[2], k0 + kr < Lk, kc, pr0, pr1);
+      if (tabk != nullptr && k0 + kr < Lk) load_cs(tabk, k0 + kr, kc, kcs);
+    } else {
+      pr0 = uint4v{0, 0, 0, 0};
+      pr1 = uint4v{0, 0, 0, 0};
+      if (k0 + vj < Lk) pr0 = *(const uint4v*)(Vb + (int64_t)(k0 + vj) * vs.s[2] + vc * 8);
+      if (k0 + vj + 1 < Lk) pr1 = *(const uint4v*)(Vb + (int64_t)(k0 + vj + 1) * vs.s[2] + vc * 8);
+    }
   };
 
   // this lane's mask bytes of a tile: 8 contiguous keys for each of its two
   // queries (qb) and halves (t)
-  auto load_mask = [&](int kt, uint2v (&mw)[2][2]) {
+  auto load_mask = [&](int kt, uint2v (&mw)[kQB][2]) {
     const int k0 = kt * kBK;
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-      const int q = q0 + wave * 32 + qb * 16 + li;
+    for (int qb = 0; qb < kQB; qb++) {
+      const int q = q0 + wave * 16 * kQB + qb * 16 + li;
       const uint8_t* mrow = mask + b * ms.s[0] + (int64_t)(q < Lq ? q : 0) * ms.s[2];
 #pragma unroll
       for (int t = 0; t < 2; t++) {
@@ -252,51 +292,68 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     }
   };
 
+  // K tile `t` (rotated, as a separate Backend.rope would store it) and the
+  // transposed V tile from the prefetch registers into LDS buffer `bf`
+  auto store_kv = [&](int t, int bf) {
+    if (kpart) {
+      store_pair<BF16, true>(pr0, pr1, tabk != nullptr && t * kBK + kr < Lk, kc, kcs, Ks[bf], kr);
+      return;
+    }
+    const uint32_t* pa = (const uint32_t*)&pr0;
+    const uint32_t* pb = (const uint32_t*)&pr1;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      uint32_t lo = (pa[e] & 0xffff) | (pb[e] << 16);
+      uint32_t hi = (pa[e] >> 16) | (pb[e] & 0xffff0000u);
+      *(uint32_t*)(Vt[bf] + vt_swz(vc * 8 + 2 * e, vj >> 3) + (vj & 7)) = lo;
+      *(uint32_t*)(Vt[bf] + vt_swz(vc * 8 + 2 * e + 1, vj >> 3) + (vj & 7)) = hi;
+    }
+  };
+
   // the first K / V tile (and its mask bytes) is requested before Q is
   // staged, so the two loads' latencies overlap
   int kt = next_tile(-1);
-  uint2v mw[2][2], mwn[2][2];
+  uint2v mw[kQB][2], mwn[kQB][2];
   if (kt < nkt) {
     prefetch(kt);
     if (mask != nullptr && tile_class(kt) == 2) load_mask(kt, mw);
   }
 
-  static_assert(kBQ * 4 == 2 * 256, "Q staging: two rounds of 256 threads");
-  // ---- stage Q (rotated) and build this wave's B fragments of Q^T; both
-  // rounds of loads are issued before the first store
-  {
-    uint4v lo[2], hi[2];
-    float2 cs[2][8];
+  // ---- stage Q (rotated); this wave's B fragments of Q^T are read below
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int t = tid + u * 256, r = t >> 2, c = t & 3, q = q0 + r;
-      load_pair(Qb + (int64_t)q * qs.s[2], q < Lq, c, lo[u], hi[u]);
-      if (tabq != nullptr && q < Lq) load_cs(tabq, q, c, cs[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int t = tid + u * 256, r = t >> 2, c = t & 3, q = q0 + r;
-      store_pair<BF16>(lo[u], hi[u], tabq != nullptr && q < Lq, c, cs[u], Qs, r);
-    }
+  for (int u = 0; u < QR; u++) {
+    const int t = tid + u * kNT, r = t >> 2, c = t & 3, q = q0 + r;
+    store_pair<BF16>(qlo[u], qhi[u], tabq != nullptr && q < Lq, c, qcs[u], Qs, r);
+  }
+  // the first tile into buffer 0; the second tile's loads start
+  int nk = nkt;
+  if (kt < nkt) {
+    store_kv(kt, 0);
+    nk = next_tile(kt);
+    if (nk < nkt) prefetch(nk);
   }
   __syncthreads();
-  uint4v qf[2][2];
+  uint4v qf[kQB][2];
 #pragma unroll
-  for (int qb = 0; qb < 2; qb++)
+  for (int qb = 0; qb < kQB; qb++)
 #pragma unroll
-    for (int s = 0; s < 2; s++) qf[qb][s] = *(const uint4v*)(Qs + qk_swz(wave * 32 + qb * 16 + li, s * 4 + g));
+    for (int s = 0; s < 2; s++)
+      qf[qb][s] = *(const uint4v*)(Qs + qk_swz(wave * 16 * kQB + qb * 16 + li, s * 4 + g));
 
 
-  float4v o[2][4];
+  float4v o[kQB][4];
+  float m[kQB], l[kQB];
 #pragma unroll
-  for (int qb = 0; qb < 2; qb++)
+  for (int qb = 0; qb < kQB; qb++) {
 #pragma unroll
     for (int d = 0; d < 4; d++) o[qb][d] = float4v{0.f, 0.f, 0.f, 0.f};
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    m[qb] = -INFINITY;
+    l[qb] = 0.f;
+  }
 
   // online softmax of one 64-key tile for query block qb: scores sv (raw,
   // -inf where hidden) -> P fragments, running max / sum, O rescale
-  uint4v pf[2][2];
+  uint4v pf[kQB][2];
   auto softmax = [&](int qb, float (&sv)[2][8], float mx) {
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -325,51 +382,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     }
   };
 
+  int buf = 0;
   while (kt < nkt) {
     const int k0 = kt * kBK;
     const int cl = tile_class(kt);
-    __syncthreads();  // the previous tile's K / V^T reads are done
-    store_pair<BF16>(klo, khi, tabk != nullptr && k0 + kr < Lk, kc, kcs, Ks, kr);
-    {
-      const uint32_t* pa = (const uint32_t*)&va;
-      const uint32_t* pb = (const uint32_t*)&vb;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        uint32_t lo = (pa[e] & 0xffff) | (pb[e] << 16);
-        uint32_t hi = (pa[e] >> 16) | (pb[e] & 0xffff0000u);
-        *(uint32_t*)(Vt + (vc * 8 + 2 * e) * kVtLd + vj) = lo;
-        *(uint32_t*)(Vt + (vc * 8 + 2 * e + 1) * kVtLd + vj) = hi;
-      }
-    }
-    __syncthreads();
-
-    // next tile's K / V (and mask bytes) one tile ahead
-    const int nk = next_tile(kt);
-    if (nk < nkt) {
-      prefetch(nk);
-      if (mask != nullptr && tile_class(nk) == 2) load_mask(nk, mwn);
-    }
+    const uint16_t* Kc = Ks[buf];
+    const uint16_t* Vc = Vt[buf];
 
     // ---- S^T = K . Q^T over 4 key blocks; block kb row i holds key
     // 32*(kb/2) + 8*(i/4) + (i%4) + 4*(kb%2) so a lane's 8 keys are contiguous
-    float4v st[2][4];
+    float4v st[kQB][4];
 #pragma unroll
     for (int kb = 0; kb < 4; kb++) {
       const int krow = 32 * (kb >> 1) + 8 * (li >> 2) + (li & 3) + 4 * (kb & 1);
-      uint4v kf0 = *(const uint4v*)(Ks + qk_swz(krow, g));
-      uint4v kf1 = *(const uint4v*)(Ks + qk_swz(krow, 4 + g));
+      uint4v kf0 = *(const uint4v*)(Kc + k_swz(krow, g));
+      uint4v kf1 = *(const uint4v*)(Kc + k_swz(krow, 4 + g));
 #pragma unroll
-      for (int qb = 0; qb < 2; qb++) {
+      for (int qb = 0; qb < kQB; qb++) {
         float4v z = {0.f, 0.f, 0.f, 0.f};
         z = mfma16<BF16>(kf0, qf[qb][0], z);
         st[qb][kb] = mfma16<BF16>(kf1, qf[qb][1], z);
       }
     }
 
+    // ---- the next tile into the other buffer (its loads were issued one
+    // tile ago), the one after it into registers, the next mask bytes
+    int nn = nkt;
+    if (nk < nkt) {
+      store_kv(nk, buf ^ 1);
+      nn = next_tile(nk);
+      if (nn < nkt) prefetch(nn);
+      if (mask != nullptr && tile_class(nk) == 2) load_mask(nk, mwn);
+    }
+
     // ---- mask (only for mixed tiles), online softmax, P fragments
     if (cl == 1) {
 #pragma unroll
-      for (int qb = 0; qb < 2; qb++) {
+      for (int qb = 0; qb < kQB; qb++) {
         float sv[2][8];
         float mx = -INFINITY;
 #pragma unroll
@@ -382,24 +431,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
         softmax(qb, sv, mx);
       }
     } else {
-      const bool in_range = k0 + kBK <= Lk;
 #pragma unroll
-      for (int qb = 0; qb < 2; qb++) {
+      for (int qb = 0; qb < kQB; qb++) {
         float sv[2][8];
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 2; t++) {
           const int kbase = k0 + 32 * t + 8 * g;  // this lane's 8 contiguous keys
+          // bit e of vis: key kbase + e is visible (mask byte nonzero, key < Lk)
+          uint32_t vis = 0xffu;
+          if (mask != nullptr) vis = mask_bits(mw[qb][t].x) | (mask_bits(mw[qb][t].y) << 4);
+          const int left = Lk - kbase;
+          if (left < 8) vis &= left > 0 ? (1u << left) - 1u : 0u;
 #pragma unroll
           for (int e = 0; e < 8; e++) {
             const float sc = e < 4 ? st[qb][2 * t][e] : st[qb][2 * t + 1][e - 4];
-            bool vis = true;
-            if (mask != nullptr) {
-              const uint32_t w = e < 4 ? mw[qb][t].x : mw[qb][t].y;
-              vis = ((w >> (8 * (e & 3))) & 0xffu) != 0;
-            }
-            if (!in_range) vis = vis && (kbase + e) < Lk;
-            sv[t][e] = vis ? sc : -INFINITY;
+            sv[t][e] = (vis >> e) & 1u ? sc : -INFINITY;
             mx = fmaxf(mx, sv[t][e]);
           }
         }
@@ -412,26 +459,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     for (int d = 0; d < 4; d++) {
 #pragma unroll
       for (int t = 0; t < 2; t++) {
-        uint4v vf = *(const uint4v*)(Vt + (d * 16 + li) * kVtLd + 32 * t + 8 * g);
+        uint4v vf = *(const uint4v*)(Vc + vt_swz(d * 16 + li, 4 * t + g));
 #pragma unroll
-        for (int qb = 0; qb < 2; qb++) o[qb][d] = mfma16<BF16>(vf, pf[qb][t], o[qb][d]);
+        for (int qb = 0; qb < kQB; qb++) o[qb][d] = mfma16<BF16>(vf, pf[qb][t], o[qb][d]);
       }
     }
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++)
+    for (int qb = 0; qb < kQB; qb++)
 #pragma unroll
       for (int t = 0; t < 2; t++) mw[qb][t] = mwn[qb][t];
+    // this tile's buffer is free and the next one complete for every wave
+    __syncthreads();
+    buf ^= 1;
     kt = nk;
+    nk = nn;
   }
 
   // ---- normalise and store (lane: one query, d = 16*dblk + 4g + 0..3)
 #pragma unroll
-  for (int qb = 0; qb < 2; qb++) {
+  for (int qb = 0; qb < kQB; qb++) {
     float lt = l[qb];
     lt += __shfl_xor(lt, 16, 64);
     lt += __shfl_xor(lt, 32, 64);
     const float inv = 1.0f / lt;
-    const int q = q0 + wave * 32 + qb * 16 + li;
+    const int q = q0 + wave * 16 * kQB + qb * 16 + li;
     if (q >= Lq) continue;
     uint16_t* op = O + b * os.s[0] + h * os.s[1] + (int64_t)q * os.s[2];
 #pragma unroll
@@ -569,11 +620,11 @@ extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, ui
     const float sl2 = scale * 1.4426950408889634f;
     dim3 grid(nqt, (unsigned)H, (unsigned)B);
     if (dt == HB_F16)
-      sdpa_mfma<false><<<grid, 256, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
+      sdpa_mfma<false><<<grid, kNT, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
                                              (const uint8_t*)mask, Ms, mask_vec, info, (uint16_t*)o, Os, (int)Lq,
                                              (int)Lk, sl2, tq, tk);
     else
-      sdpa_mfma<true><<<grid, 256, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
+      sdpa_mfma<true><<<grid, kNT, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
                                             (const uint8_t*)mask, Ms, mask_vec, info, (uint16_t*)o, Os, (int)Lq,
                                             (int)Lk, sl2, tq, tk);
     check_launch("hb_sdpa");

@@ -683,8 +683,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // into (al, bl); stages the W tile of g+1 (held in bs) into the other buffer.
   auto step = [&](int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl, BRegs& bs) {
     // the residual tile arrives while the tile computes, once the previous
-    // tile's output has left the C tile
-    if (R != nullptr && kin == res_stage) dma_resid(tile_m0(it_cur), tile_n0(it_cur));
+    // tile's output has left the C tile (at once for a block's first tile)
+    if (R != nullptr && kin == (it_cur == 0 ? 0 : res_stage)) dma_resid(tile_m0(it_cur), tile_n0(it_cur));
     const int g2 = g + 2 < S ? g + 2 : S - 1;
     const int i2 = g2 / KT, k2 = (g2 - i2 * KT) * BK;
     load_a(tile_m0(i2), k2, al);
