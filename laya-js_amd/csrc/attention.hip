@@ -44,43 +44,53 @@ constexpr int kMaxKeyTiles = 1024;  // Lk <= 65536 on the MFMA path
 
 // ------------------------------------------------------------------ mask summary
 
-// Class of every (batch, 128-query tile, 64-key tile) block of a bool mask:
+// Class of every (batch, 16-query group, 64-key tile) block of a bool mask:
 // 0 = no visible key (skipped), 1 = every key visible (no mask reads),
-// 2 = mixed or running past Lk (per-element mask).  Computed once per mask
-// tensor and reused by every layer that attends with it.
+// 2 = mixed or running past Lk (per-element mask).  One byte per group, the
+// 8 groups of a 128-query tile together: cls[((b * nqt + qt) * nkt + kt) * 8
+// + group].  Computed once per mask tensor and reused by every layer that
+// attends with it; the attention kernel skips a key tile for a wave whose
+// group has class 0 and stages it only if some group needs it.
 __global__ __launch_bounds__(256) void mask_class_kernel(const uint8_t* __restrict__ mask, S4 ms, int Lq, int Lk,
                                                          int nqt, int nkt, uint8_t* __restrict__ cls, int vec) {
+  __shared__ int anyg[kNW], allg[kNW];
   const int kt = blockIdx.x, qt = blockIdx.y, b = blockIdx.z;
   const int q0 = qt * kBQ, k0 = kt * kBK;
   const int nq = min(kBQ, Lq - q0), nk = min(kBK, Lk - k0);
-  const int qn = ms.s[2] == 0 ? 1 : nq;  // a [B,1,1,L] mask has one row for every query
-  int any = 0, all = 1;
+  const bool bcast = ms.s[2] == 0;  // a [B,1,1,L] mask has one row for every query
+  if (threadIdx.x < kNW) {
+    anyg[threadIdx.x] = 0;
+    allg[threadIdx.x] = 1;
+  }
+  __syncthreads();
   if (vec && nk == kBK) {
-    // 16-byte rows chunks: qn rows x 4 chunks
-    for (int i = threadIdx.x; i < qn * 4; i += blockDim.x) {
-      int q = i >> 2, c = i & 3;
-      uint4v w = *(const uint4v*)(mask + b * ms.s[0] + (int64_t)(q0 + q) * ms.s[2] + k0 + c * 16);
-      // bytes are 0/1: any byte set <=> word != 0; all set <=> every byte == 1
-      uint32_t o = w.x | w.y | w.z | w.w, a = w.x & w.y & w.z & w.w;
-      any |= o != 0;
-      all &= a == 0x01010101u;
+    // 16-byte row chunks: rows x 4 chunks
+    for (int i = threadIdx.x; i < nq * 4; i += blockDim.x) {
+      const int q = i >> 2, c = i & 3;
+      const uint4v w = *(const uint4v*)(mask + b * ms.s[0] + (int64_t)(bcast ? 0 : q0 + q) * ms.s[2] + k0 + c * 16);
+      // any byte nonzero <=> word != 0; all visible when every byte == 1
+      const uint32_t o = w.x | w.y | w.z | w.w, a = w.x & w.y & w.z & w.w;
+      if (o != 0) atomicOr(&anyg[q >> 4], 1);
+      if (a != 0x01010101u) atomicAnd(&allg[q >> 4], 0);
     }
   } else {
-    for (int i = threadIdx.x; i < qn * nk; i += blockDim.x) {
-      int q = i / nk, k = i - q * nk;
-      uint8_t m = mask[b * ms.s[0] + (int64_t)(q0 + q) * ms.s[2] + (int64_t)(k0 + k) * ms.s[3]];
-      any |= m != 0;
-      all &= m != 0;
+    for (int i = threadIdx.x; i < nq * nk; i += blockDim.x) {
+      const int q = i / nk, k = i - q * nk;
+      const uint8_t m = mask[b * ms.s[0] + (int64_t)(bcast ? 0 : q0 + q) * ms.s[2] + (int64_t)(k0 + k) * ms.s[3]];
+      if (m != 0) atomicOr(&anyg[q >> 4], 1);
+      else atomicAnd(&allg[q >> 4], 0);
     }
   }
-  any = __syncthreads_or(any);
-  all = __syncthreads_and(all);
-  if (threadIdx.x == 0) cls[((int64_t)b * nqt + qt) * nkt + kt] = !any ? 0 : (all && nk == kBK ? 1 : 2);
+  __syncthreads();
+  if (threadIdx.x < kNW) {
+    const int g = threadIdx.x;
+    cls[(((int64_t)b * nqt + qt) * nkt + kt) * kNW + g] = !anyg[g] ? 0 : (allg[g] && nk == kBK ? 1 : 2);
+  }
 }
 
 static size_t mask_info_bytes(int64_t B, int64_t Lq, int64_t Lk) {
   int64_t nqt = (Lq + kBQ - 1) / kBQ, nkt = (Lk + kBK - 1) / kBK;
-  return (size_t)(B * nqt * nkt);
+  return (size_t)(B * nqt * nkt * kNW);
 }
 
 static void launch_mask_info(hipStream_t st, const uint8_t* mask, const S4& ms, int64_t B, int64_t Lq, int64_t Lk,
@@ -202,7 +212,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ * 64];
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * 64];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64 * kVtLd];
-  __shared__ uint8_t cls_row[kMaxKeyTiles];
+  __shared__ uint16_t cls_row[kMaxKeyTiles];  // 2 bits of class per 16-query group
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
@@ -226,19 +236,30 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
     if (tabq != nullptr && q < Lq) load_cs(tabq, q, c, qcs[u]);
   }
 
-  // tile classes of this (b, query tile): 0 skip, 1 all visible, 2 per-element
-  // mask / key bound; staged in LDS once (the host caps nkt at kMaxKeyTiles)
+  // tile classes of this (b, query tile) for each wave's 16-query group: 0
+  // skip, 1 all visible, 2 per-element mask / key bound; staged in LDS once
+  // (the host caps nkt at kMaxKeyTiles).  A tile is staged when some group
+  // needs it.
+  static_assert(kQB == 1 && kNW == 8, "one 16-query group per wave, 8 per tile");
   for (int t = tid; t < nkt; t += kNT) {
-    uint8_t c;
-    if (cls != nullptr) c = cls[((int64_t)b * nqt + qt) * nkt + t];
-    else if (mask != nullptr) c = 2;
-    else c = (t + 1) * kBK <= Lk ? 1 : 2;
-    cls_row[t] = c;
+    uint32_t c;
+    if (cls != nullptr) {
+      const uint2v w = *(const uint2v*)(cls + (((int64_t)b * nqt + qt) * nkt + t) * kNW);
+      c = 0;
+#pragma unroll
+      for (int gq = 0; gq < kNW; gq++) c |= (((gq < 4 ? w.x : w.y) >> (8 * (gq & 3))) & 3u) << (2 * gq);
+    } else if (mask != nullptr) {
+      c = 0xAAAAu;
+    } else {
+      c = (t + 1) * kBK <= Lk ? 0x5555u : 0xAAAAu;
+    }
+    cls_row[t] = (uint16_t)c;
   }
-  auto tile_class = [&](int kt) -> int { return cls_row[kt]; };
+  auto tile_needed = [&](int kt) -> bool { return cls_row[kt] != 0; };
+  auto wave_class = [&](int kt) -> int { return (cls_row[kt] >> (2 * wave)) & 3; };
   auto next_tile = [&](int kt) -> int {
     kt++;
-    while (kt < nkt && tile_class(kt) == 0) kt++;
+    while (kt < nkt && !tile_needed(kt)) kt++;
     return kt;
   };
   __syncthreads();  // the class row is complete
@@ -316,7 +337,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
   uint2v mw[kQB][2], mwn[kQB][2];
   if (kt < nkt) {
     prefetch(kt);
-    if (mask != nullptr && tile_class(kt) == 2) load_mask(kt, mw);
+    if (mask != nullptr && wave_class(kt) == 2) load_mask(kt, mw);
   }
 
   // ---- stage Q (rotated); this wave's B fragments of Q^T are read below
@@ -385,15 +406,17 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
   int buf = 0;
   while (kt < nkt) {
     const int k0 = kt * kBK;
-    const int cl = tile_class(kt);
+    const int cl = wave_class(kt);  // this wave's class of the tile
     const uint16_t* Kc = Ks[buf];
     const uint16_t* Vc = Vt[buf];
 
     // ---- S^T = K . Q^T over 4 key blocks; block kb row i holds key
     // 32*(kb/2) + 8*(i/4) + (i%4) + 4*(kb%2) so a lane's 8 keys are contiguous
+    // (a wave whose queries see no key of the tile skips its MFMAs and softmax)
     float4v st[kQB][4];
 #pragma unroll
     for (int kb = 0; kb < 4; kb++) {
+      if (cl == 0) break;
       const int krow = 32 * (kb >> 1) + 8 * (li >> 2) + (li & 3) + 4 * (kb & 1);
       uint4v kf0 = *(const uint4v*)(Kc + k_swz(krow, g));
       uint4v kf1 = *(const uint4v*)(Kc + k_swz(krow, 4 + g));
@@ -412,11 +435,12 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
       store_kv(nk, buf ^ 1);
       nn = next_tile(nk);
       if (nn < nkt) prefetch(nn);
-      if (mask != nullptr && tile_class(nk) == 2) load_mask(nk, mwn);
+      if (mask != nullptr && wave_class(nk) == 2) load_mask(nk, mwn);
     }
 
     // ---- mask (only for mixed tiles), online softmax, P fragments
-    if (cl == 1) {
+    if (cl == 0) {
+    } else if (cl == 1) {
 #pragma unroll
       for (int qb = 0; qb < kQB; qb++) {
         float sv[2][8];
@@ -457,6 +481,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
     // ---- O^T += V^T . P^T
 #pragma unroll
     for (int d = 0; d < 4; d++) {
+      if (cl == 0) break;
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         uint4v vf = *(const uint4v*)(Vc + vt_swz(d * 16 + li, 4 * t + g));
