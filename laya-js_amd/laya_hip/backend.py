@@ -152,15 +152,20 @@ def _panel_rows(M: int) -> int:
 class _PanelRows:
     """The value of a tensor, an [M, K] 16-bit matrix, held in panel order
     (rows padded to a multiple of 32) in `st`, written for a large-M linear
-    layer.  Other readers get a row-major copy (HipBackend._ready)."""
+    layer.  Other readers get a row-major copy (HipBackend._ready): the
+    LayerNorm it came from run again row-major (`norm`, same bits), or an
+    unpack of the panel."""
 
-    def __init__(self, st, M: int, K: int):
-        self.st, self.M, self.K = st, M, K
+    def __init__(self, st, M: int, K: int, norm: Optional["_PendingNorm"] = None):
+        self.st, self.M, self.K, self.norm = st, M, K, norm
 
     def release(self):
         if self.st is not None:
             self.st.release()
             self.st = None
+        if self.norm is not None:
+            self.norm.release()
+            self.norm = None
 
 
 class _PendingNorm:
@@ -429,8 +434,14 @@ class HipBackend:
         elif isinstance(lz, _PanelRows):
             st = self._malloc(_numel(t.shape) * DT[t.dtype][1])
             t._st, t._off, t._strides = st, 0, _contig(t.shape)
-            self.stats["panel_unpacks"] += 1
-            self._call("read", "hb_panel_unpack", self.ctx, lz.st.ptr, st.ptr, lz.K, lz.M, lz.K)
+            if lz.norm is not None:
+                nm = lz.norm
+                dtx, xp, ld, dtw, wp, bp = nm.args
+                self._call("layerNorm", "hb_layernorm", self.ctx, dtx, xp, ld, dtw, wp, bp, DT[nm.dt][0], st.ptr,
+                           nm.rows, nm.D, nm.eps)
+            else:
+                self.stats["panel_unpacks"] += 1
+                self._call("read", "hb_panel_unpack", self.ctx, lz.st.ptr, st.ptr, lz.K, lz.M, lz.K)
             lz.release()
         elif isinstance(lz, _PendingRope):
             src_st, off, strides, dtype, shape = lz.src
@@ -455,8 +466,7 @@ class HipBackend:
             dtx, xp, ld, dtw, wp, bp = lz.args
             self._call("layerNorm", "hb_layernorm_panel", self.ctx, dtx, xp, ld, dtw, wp, bp, st.ptr, lz.rows, lz.D,
                        lz.eps)
-            lz.release()
-            x._lazy = _PanelRows(st, lz.rows, lz.D)
+            x._lazy = _PanelRows(st, lz.rows, lz.D, norm=lz)  # keeps the LayerNorm's operands
             return x._lazy
         if (isinstance(lz, _PendingLinear) and lz.epi == F.HB_EPI_GEGLU and lz.arow_ok and lz.n_out % 64 == 0):
             M = lz.x[1]
