@@ -289,7 +289,7 @@ def run_gemm_sweep(args) -> None:
             for kind, fn in kinds:
                 def launch():
                     y = fn()
-                    return be.geglu(y) if geglu else be._ready(y)
+                    return be._ready(be.geglu(y) if geglu else y)  # launched now, not left pending
                 for _ in range(3):
                     be.dispose(launch())
                 reps = max(5, int(2e11 / (2 * M * N * K)))
