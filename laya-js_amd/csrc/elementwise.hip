@@ -175,7 +175,7 @@ __global__ void geglu_kernel(int dt_x, const void* __restrict__ x, int64_t ldx, 
     int64_t r = i / F, j = i - r * F;
     float v = load_f(x, r * ldx + j, dt_x);
     float g = load_f(x, r * ldx + F + j, dt_x);
-    store_f(y, i, dt_y, (fast ? gelu_fast(v) : gelu_erf(v)) * g);
+    store_f(y, i, dt_y, pin_f32((fast ? gelu_fast(v) : gelu_erf(v)) * g));
   }
 }
 

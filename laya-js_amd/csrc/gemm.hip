@@ -338,7 +338,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
           float v = to_f<BF16>(from_f<BF16>(acc[i][j][4 * g + e] + bv));
           if constexpr (GEGLU) {
             const float gt = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][4 * g + e] + bg));
-            v = gelu_fast(v) * gt;
+            v = pin_f32(gelu_fast(v) * gt);  // the f32 product, then one rounding to the storage type
           }
           o[e] = from_f<BF16>(v);
         }
@@ -577,7 +577,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const float a = HB ? acc[i][j][4 * g + e] + bv[e] : acc[i][j][4 * g + e];
             if constexpr (GEGLU) {
               const float ag = HB ? acc[i][j + TN / 2][4 * g + e] + bg[e] : acc[i][j + TN / 2][4 * g + e];
-              o[e] = from_f<BF16>(gelu_fast(to_f<BF16>(from_f<BF16>(a))) * to_f<BF16>(from_f<BF16>(ag)));
+              o[e] = from_f<BF16>(pin_f32(gelu_fast(to_f<BF16>(from_f<BF16>(a))) * to_f<BF16>(from_f<BF16>(ag))));
             } else {
               o[e] = from_f<BF16>(a);
             }
@@ -607,6 +607,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     c = nb * 2 + h;
     return ((int64_t)rb * yblk + nb) * 512 + (h * 32 + r32) * 8;  // relative to the tile's first block
   };
+  // output chunk c of C tile row r
+  auto out_chunk = [&](int r, int c) __attribute__((always_inline)) -> uint4v {
+    return *(const uint4v*)(Cs + r_slot(r, c) * 8);
+  };
   auto write_out = [&](int m0, int n0) {
     int t0 = tid;
     asm volatile("" : "+v"(t0));
@@ -617,7 +621,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         int r, c;
         const int64_t o = panel_chunk(q, r, c);
         if ((r >> 5) >= rbl || n0 + c * 8 >= N) continue;
-        *(uint4v*)(yb + o) = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+        *(uint4v*)(yb + o) = out_chunk(r, c);
       }
       return;
     }
@@ -626,7 +630,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int k = 0; k < BM * CPR / NT; k++) {
         const int q = t0 + k * NT, r = q / CPR, c = q - r * CPR;
-        *(uint4v*)(yb + (int64_t)r * ldy + c * 8) = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+        *(uint4v*)(yb + (int64_t)r * ldy + c * 8) = out_chunk(r, c);
       }
       return;
     }
@@ -634,7 +638,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int r = q / CPR, c = q - r * CPR;
       const int gm = m0 + r, gn = n0 + c * 8;
       if (gm >= M || gn >= N) continue;
-      const uint4v v = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+      const uint4v v = out_chunk(r, c);
       uint16_t* yp = Y + (int64_t)gm * ldy + gn;
       if (gn + 8 <= N) {
         *(uint4v*)yp = v;
@@ -656,24 +660,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const bool spread = KT >= 2 * WO_STAGES;
   const int res_stage = spread ? WO_STAGES : 0;
   int wo_m0 = -1, wo_n0 = 0, it_cur = 0;  // wo_m0 < 0: no output pending
-  auto write_part = [&](int part) {
+  // part `part` (0..WO_STAGES-1) of the pending output; the values are
+  // computed in every tile's first stages (branch-free, between the MFMAs)
+  // and stored only when an output is pending (the block's first tile has
+  // none: its C tile then holds nothing of use)
+  auto write_part = [&](int part) __attribute__((always_inline)) {
     int t0 = tid;
     asm volatile("" : "+v"(t0));
-    if (ypan) {
-      uint16_t* yb = Y + ((int64_t)(wo_m0 >> 5) * yblk + (wo_n0 >> 4)) * 512;
-#pragma unroll
-      for (int k = 0; k < PER_STAGE; k++) {
-        int r, c;
-        const int64_t o = panel_chunk(t0 + (part * PER_STAGE + k) * NT, r, c);
-        *(uint4v*)(yb + o) = *(const uint4v*)(Cs + r_slot(r, c) * 8);
-      }
-      return;
-    }
-    uint16_t* yb = Y + (int64_t)wo_m0 * ldy + wo_n0;
+    uint4v v[PER_STAGE];
+    int64_t off[PER_STAGE];
 #pragma unroll
     for (int k = 0; k < PER_STAGE; k++) {
-      const int q = t0 + (part * PER_STAGE + k) * NT, r = q / CPR, c = q - r * CPR;
-      *(uint4v*)(yb + (int64_t)r * ldy + c * 8) = *(const uint4v*)(Cs + r_slot(r, c) * 8);
+      const int q = t0 + (part * PER_STAGE + k) * NT;
+      int r, c;
+      if (ypan) {
+        off[k] = panel_chunk(q, r, c);
+      } else {
+        r = q / CPR;
+        c = q - r * CPR;
+        off[k] = (int64_t)r * ldy + c * 8;
+      }
+      v[k] = out_chunk(r, c);
+    }
+    if (wo_m0 >= 0) {
+      uint16_t* yb = ypan ? Y + ((int64_t)(wo_m0 >> 5) * yblk + (wo_n0 >> 4)) * 512 : Y + (int64_t)wo_m0 * ldy + wo_n0;
+#pragma unroll
+      for (int k = 0; k < PER_STAGE; k++) *(uint4v*)(yb + off[k]) = v[k];
     }
   };
 
@@ -681,7 +693,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   BRegs B0, B1;
   // step g: MFMAs on `ac` and LDS buffer g&1; loads stage g+2 of the stream
   // into (al, bl); stages the W tile of g+1 (held in bs) into the other buffer.
-  auto step = [&](int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl, BRegs& bs) {
+  // WP: this stage also writes part `kin` of the previous tile's output
+  // (branch-free inside the stage, so the scheduler can put its LDS reads,
+  // VALU work and stores between the MFMAs)
+  auto step = [&](auto wp, int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl,
+                  BRegs& bs) __attribute__((always_inline)) {
+    constexpr bool WP = decltype(wp)::value;
     // the residual tile arrives while the tile computes, once the previous
     // tile's output has left the C tile (at once for a block's first tile)
     if (R != nullptr && kin == (it_cur == 0 ? 0 : res_stage)) dma_resid(tile_m0(it_cur), tile_n0(it_cur));
@@ -701,23 +718,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int j = 0; j < TN; j++)
 #pragma unroll
         for (int i = 0; i < TM; i++) acc[i][j] = mfma32<BF16>(bf[s][j], ac[i][s], acc[i][j]);
+    if constexpr (WP) write_part(kin);
     // schedule: substep-0 fragment reads, then MFMA pairs, each preceded by
     // one global load (while any remain) and one fragment read of the next
-    // substep; the W staging for the next stage goes last
+    // substep (and, writing out, a share of the VALU work); the W staging for
+    // the next stage goes last
     constexpr int NVMEM = TM * KS + B_LD, NPAIR = KS * TN;
+    constexpr int NVALU = WP ? 1 : 0;
     __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
 #pragma unroll
     for (int p = 0; p < NPAIR; p++) {
       if (p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       if (p < (KS - 1) * TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (NVALU) __builtin_amdgcn_sched_group_barrier(0x002, NVALU, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
     }
     store_b((g + 1) & 1, bs);
     __builtin_amdgcn_sched_group_barrier(0x200, B_LD, 0);
-    // a sixth of the previous tile's output, issued after this stage's loads
-    // and after the wait for the previous stage's: the stores then only have
-    // to complete by the wait two stages on
-    if (wo_m0 >= 0 && kin < WO_STAGES) write_part(kin);
     __syncthreads();
   };
 
@@ -736,15 +753,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   for (int it = 0; it < ntile; it++) {
     const int g0 = it * KT;
     it_cur = it;
-    for (int kt = 0; kt < KT; kt += 6) {
-      step(g0 + kt, kt, A0, A2, B0, B1);
-      if (kt + 1 < KT) step(g0 + kt + 1, kt + 1, A1, A0, B1, B0);
-      if (kt + 2 < KT) step(g0 + kt + 2, kt + 2, A2, A1, B0, B1);
-      if (kt + 3 < KT) step(g0 + kt + 3, kt + 3, A0, A2, B1, B0);
-      if (kt + 4 < KT) step(g0 + kt + 4, kt + 4, A1, A0, B0, B1);
-      if (kt + 5 < KT) step(g0 + kt + 5, kt + 5, A2, A1, B1, B0);
-      if (kt == 0) wo_m0 = -1;  // the previous tile's output has left
-    }
+    // six stages (the register rotation's period); with WP, stages 0..5 of
+    // the tile, each writing a sixth of the previous tile's output
+    auto six = [&](auto wp, int kt) __attribute__((always_inline)) {
+      step(wp, g0 + kt, kt, A0, A2, B0, B1);
+      if (kt + 1 < KT) step(wp, g0 + kt + 1, kt + 1, A1, A0, B1, B0);
+      if (kt + 2 < KT) step(wp, g0 + kt + 2, kt + 2, A2, A1, B0, B1);
+      if (kt + 3 < KT) step(wp, g0 + kt + 3, kt + 3, A0, A2, B1, B0);
+      if (kt + 4 < KT) step(wp, g0 + kt + 4, kt + 4, A1, A0, B0, B1);
+      if (kt + 5 < KT) step(wp, g0 + kt + 5, kt + 5, A2, A1, B1, B0);
+    };
+    six(std::true_type{}, 0);  // stages 0..5 write the previous tile's output, if pending
+    wo_m0 = -1;
+    for (int kt = 6; kt < KT; kt += 6) six(std::false_type{}, kt);
     // the residual DMA (stage res_stage < KT - 1) has landed once at most the
     // W and A loads of one stage are outstanding (they were all issued after
     // it, and loads complete in order); the barrier makes every wave's part
