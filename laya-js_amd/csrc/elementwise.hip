@@ -194,6 +194,27 @@ __global__ void gather_kernel(int dt, const void* __restrict__ table, int64_t V,
   }
 }
 
+// bytes of one element of a dtype code
+static int dt_size(int dt) {
+  return (dt == HB_F32 || dt == HB_I32 || dt == HB_U32) ? 4
+         : (dt == HB_F16 || dt == HB_BF16 || dt == HB_U16 || dt == HB_I16) ? 2 : 1;
+}
+
+// Same-dtype gather of whole 16-byte chunks (rows of D * elem bytes, a
+// multiple of 16): one thread per chunk, a bit copy.
+__global__ void gather16_kernel(const uint8_t* __restrict__ table, int64_t V, int64_t row_bytes,
+                                const int32_t* __restrict__ ids, int64_t n, int64_t batch_rows,
+                                uint8_t* __restrict__ out) {
+  const int64_t cpr = row_bytes >> 4, total = n * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cpr, c = i - r * cpr;
+    int64_t id = ids[r];
+    id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+    const int64_t base = batch_rows > 0 ? (r / batch_rows) * V : 0;
+    ((uint4v*)out)[i] = *(const uint4v*)(table + (base + id) * row_bytes + c * 16);
+  }
+}
+
 __global__ void meanpool_kernel(int dt_x, const void* __restrict__ x, const uint8_t* __restrict__ mask, int64_t B,
                                 int64_t L, int64_t D, float* __restrict__ out) {
   int64_t total = B * D;
@@ -362,8 +383,7 @@ int hb_unary(uintptr_t ctx, int op, int dt_x, uintptr_t x, const int64_t* xs, in
       if (shape[d] != 1 && xs[d] != expect) contig = false;
       expect *= shape[d];
     }
-    int es = (dt_x == HB_F32 || dt_x == HB_I32 || dt_x == HB_U32) ? 4
-             : (dt_x == HB_F16 || dt_x == HB_BF16 || dt_x == HB_U16 || dt_x == HB_I16) ? 2 : 1;
+    int es = dt_size(dt_x);
     if (contig && ((n * es) % 16 == 0) && (x % 16 == 0) && (y % 16 == 0)) {
       int64_t n16 = n * es / 16;
       copy_bytes_kernel<<<grid_for(n16, 256), 256, 0, st>>>((const uint4v*)x, (uint4v*)y, n16);
@@ -422,6 +442,13 @@ int hb_gather(uintptr_t ctx, int dt, uintptr_t table, int64_t V, int64_t D, uint
   HB_REQUIRE(V > 0 || n == 0, "hb_gather: empty table");
   int64_t total = n * D;
   if (total == 0) return 0;
+  const int es = dt_size(dt);
+  if (dt == dt_out && (D * es) % 16 == 0 && table % 16 == 0 && out % 16 == 0) {
+    gather16_kernel<<<grid_for(n * (D * es / 16), 256), 256, 0, stream_of(ctx)>>>(
+        (const uint8_t*)table, V, D * es, (const int32_t*)ids, n, batch_rows, (uint8_t*)out);
+    check_launch("hb_gather");
+    return 0;
+  }
   gather_kernel<<<grid_for(total, 256), 256, 0, stream_of(ctx)>>>(dt, (const void*)table, V, D,
                                                                    (const int32_t*)ids, n, batch_rows, dt_out,
                                                                    (void*)out);
