@@ -230,6 +230,17 @@ int hb_rope(uintptr_t ctx, int dt_x, uintptr_t x, const int64_t* xs, int dt_y, u
 int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks, uintptr_t v,
             const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info, uintptr_t o, const int64_t* os,
             int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, float scale, double rope_q, double rope_k);
+
+/* hb_sdpa with o written in panel order (HB_X_PANEL above) as the [B*Lq,
+ * H*D] matrix whose row b*Lq + l holds the heads side by side: the layout
+ * modernbert's transpose + reshape of the attention output
+ * (modernbert/src/index.ts:352) feeds to attn Wo, for a large-M Wo that reads
+ * it with HB_X_PANEL.  Same arithmetic as hb_sdpa; needs its MFMA path
+ * (f16/bf16, D = 64, aligned operands, a mask that does not vary over heads)
+ * and a 16-byte aligned o of ceil(B*Lq/32)*32 rows. */
+int hb_sdpa_panel(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks, uintptr_t v,
+                  const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info, uintptr_t o, int64_t B,
+                  int64_t H, int64_t Lq, int64_t Lk, int64_t D, float scale, double rope_q, double rope_k);
 /* Size of a mask summary for (B, Lq, Lk). */
 int hb_sdpa_mask_info_bytes(int64_t B, int64_t Lq, int64_t Lk, size_t* bytes);
 /* Summarises a bool attention mask (strides ms[4] over [B,H,Lq,Lk], head

@@ -207,7 +207,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
                                                  const uint8_t* __restrict__ mask, S4 ms, int mask_vec,
                                                  const uint8_t* __restrict__ cls, uint16_t* __restrict__ O, S4 os,
                                                  int Lq, int Lk, float scale_log2, const float2* __restrict__ tabq,
-                                                 const float2* __restrict__ tabk) {
+                                                 const float2* __restrict__ tabk, int pK) {
   // Q, and two buffers of K and V^T: tile t + 1 is staged while tile t computes
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ * 64];
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * 64];
@@ -509,13 +509,25 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
     const float inv = 1.0f / lt;
     const int q = q0 + wave * 16 * kQB + qb * 16 + li;
     if (q >= Lq) continue;
-    uint16_t* op = O + b * os.s[0] + h * os.s[1] + (int64_t)q * os.s[2];
+    // strided [B, H, Lq, D], or (pK > 0) panel order of the [B*Lq, pK]
+    // matrix whose row b*Lq + q holds the heads side by side: columns
+    // 64h + 16d + 4g.. are 16-column block 4h + d, half g/2, offset 4(g%2)
+    uint16_t* op;
+    int64_t dstep;
+    if (pK > 0) {
+      const int64_t m = (int64_t)b * Lq + q;
+      op = O + ((m >> 5) * (pK >> 4) + 4 * h) * 512 + ((g >> 1) * 32 + (m & 31)) * 8 + 4 * (g & 1);
+      dstep = 512;
+    } else {
+      op = O + b * os.s[0] + h * os.s[1] + (int64_t)q * os.s[2] + 4 * g;
+      dstep = 16;
+    }
 #pragma unroll
     for (int d = 0; d < 4; d++) {
       uint2v w;
       w.x = fromf<BF16>(o[qb][d][0] * inv) | (fromf<BF16>(o[qb][d][1] * inv) << 16);
       w.y = fromf<BF16>(o[qb][d][2] * inv) | (fromf<BF16>(o[qb][d][3] * inv) << 16);
-      *(uint2v*)(op + d * 16 + 4 * g) = w;
+      *(uint2v*)(op + d * dstep) = w;
     }
   }
 }
@@ -605,17 +617,17 @@ extern "C" int hb_sdpa_mask_info(uintptr_t ctx, uintptr_t mask, const int64_t* m
   HB_API_END
 }
 
-extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
-                       uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info,
-                       uintptr_t o, const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
-                       float scale, double rope_q, double rope_k) {
-  HB_API_BEGIN
+// pK > 0: o is the panel-order [B*Lq, pK] matrix (pK = H*D), MFMA path only
+static void sdpa_impl(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
+                      uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info,
+                      uintptr_t o, const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
+                      float scale, double rope_q, double rope_k, int pK) {
   HB_REQUIRE(dt == HB_F32 || dt == HB_F16 || dt == HB_BF16, "hb_sdpa: dtype must be f32, f16 or bf16");
   HB_REQUIRE(qs && ks && vs && os, "hb_sdpa: null strides");
   HB_REQUIRE(!mask || ms, "hb_sdpa: mask without strides");
   HB_REQUIRE(B >= 0 && H >= 0 && Lq >= 0 && Lk >= 0 && D > 0, "hb_sdpa: bad shape");
   HB_REQUIRE(B < 65536 && H < 65536 && Lq < (1 << 30) && Lk < (1 << 30), "hb_sdpa: shape too large");
-  if (B == 0 || H == 0 || Lq == 0) return 0;
+  if (B == 0 || H == 0 || Lq == 0) return;
   HB_REQUIRE((rope_q <= 0 && rope_k <= 0) || D % 2 == 0, "hb_sdpa: rope needs an even head dim");
   hipStream_t st = stream_of(ctx);
   const float2* tq = rope_q > 0 ? (const float2*)rope_table(ctx, Lq, D, rope_q) : nullptr;
@@ -626,6 +638,9 @@ extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, ui
               vs[2] % 8 == 0 && qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 &&
               vs[0] % 8 == 0 && vs[1] % 8 == 0 && os[0] % 4 == 0 && os[1] % 4 == 0 && os[2] % 4 == 0 &&
               (mask == 0 || ms[1] == 0) && (Lk + kBK - 1) / kBK <= kMaxKeyTiles;
+  if (pK > 0)
+    HB_REQUIRE(fast && o % 16 == 0 && pK == H * D,
+               "hb_sdpa_panel: needs the MFMA path (f16/bf16, D = 64, aligned operands, mask not varying over heads)");
   if (fast) {
     int nqt = (int)((Lq + kBQ - 1) / kBQ);
     uint8_t* info = (uint8_t*)mask_info;
@@ -647,11 +662,11 @@ extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, ui
     if (dt == HB_F16)
       sdpa_mfma<false><<<grid, kNT, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
                                              (const uint8_t*)mask, Ms, mask_vec, info, (uint16_t*)o, Os, (int)Lq,
-                                             (int)Lk, sl2, tq, tk);
+                                             (int)Lk, sl2, tq, tk, pK);
     else
       sdpa_mfma<true><<<grid, kNT, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
                                             (const uint8_t*)mask, Ms, mask_vec, info, (uint16_t*)o, Os, (int)Lq,
-                                            (int)Lk, sl2, tq, tk);
+                                            (int)Lk, sl2, tq, tk, pK);
     check_launch("hb_sdpa");
     if (tmp) pool_free(ctx, tmp);
   } else {
@@ -665,5 +680,24 @@ extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, ui
                                      tq, tk);
     check_launch("hb_sdpa(generic)");
   }
+}
+
+extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
+                       uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info,
+                       uintptr_t o, const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
+                       float scale, double rope_q, double rope_k) {
+  HB_API_BEGIN
+  sdpa_impl(ctx, dt, q, qs, k, ks, v, vs, mask, ms, mask_info, o, os, B, H, Lq, Lk, D, scale, rope_q, rope_k, 0);
+  HB_API_END
+}
+
+extern "C" int hb_sdpa_panel(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
+                             uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info,
+                             uintptr_t o, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, float scale,
+                             double rope_q, double rope_k) {
+  HB_API_BEGIN
+  const int64_t os[4] = {0, 0, 0, 1};  // unused: the output is addressed in panel order
+  sdpa_impl(ctx, dt, q, qs, k, ks, v, vs, mask, ms, mask_info, o, os, B, H, Lq, Lk, D, scale, rope_q, rope_k,
+            (int)(H * D));
   HB_API_END
 }

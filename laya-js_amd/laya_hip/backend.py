@@ -305,6 +305,64 @@ class _PendingRope:
             self.ref = None
 
 
+class _PendingSdpa:
+    """sdpa not yet launched (index.ts:230-237).  The result and the views
+    taken of it (transpose / reshape keep their strides over the output's
+    physical [B, Lq, H, D] storage) share this object; the first reader
+    launches it: row-major for most, or in panel order for a large-M linear
+    layer reading the contiguous [B*Lq, H*D] view (modernbert's merged
+    heads into attn Wo).  Holds a reference on every operand's storage."""
+
+    def __init__(self, be, args, refs, panel_ok: bool):
+        self.be, self.args, self.refs, self.panel_ok = be, args, refs, panel_ok
+        self.users = 1
+        self.st = None  # the row-major output, once launched
+        dtc, *_rest = args
+        B, H, Lq, D = args[10], args[11], args[12], args[14]
+        self.M, self.K, self.es = B * Lq, H * D, 4 if dtc == F.HB_F32 else 2
+
+    def share(self) -> "_PendingSdpa":
+        self.users += 1
+        return self
+
+    def release(self):
+        self.users -= 1
+        if self.users == 0:
+            for s in self.refs:
+                s.release()
+            self.refs = []
+            if self.st is not None:
+                self.st.release()
+                self.st = None
+
+    def _count(self):
+        be = self.be
+        be.stats["sdpa"] += 1
+        if self.args[16] or self.args[17]:
+            be.stats["sdpa_fused_rope"] += 1
+
+    def rowmajor(self):
+        if self.st is None:
+            be = self.be
+            dtc, qp, qs, kp, ks, vp, vs, mp, ms, info, B, H, Lq, Lk, D, scale, rq, rk = self.args
+            self.st = be._malloc(B * Lq * H * D * self.es)
+            if B * H * Lq:
+                self._count()
+                be._call("sdpa", "hb_sdpa", be.ctx, dtc, qp, F.i64s(qs), kp, F.i64s(ks), vp, F.i64s(vs), mp,
+                         F.i64s(ms) if ms is not None else None, info, self.st.ptr, F.i64s((Lq * H * D, D, H * D, 1)),
+                         B, H, Lq, Lk, D, float(scale), rq, rk)
+        return self.st
+
+    def panel(self):
+        be = self.be
+        dtc, qp, qs, kp, ks, vp, vs, mp, ms, info, B, H, Lq, Lk, D, scale, rq, rk = self.args
+        st = be._malloc(_panel_rows(self.M) * self.K * self.es)
+        self._count()
+        be._call("sdpa", "hb_sdpa_panel", be.ctx, dtc, qp, F.i64s(qs), kp, F.i64s(ks), vp, F.i64s(vs), mp,
+                 F.i64s(ms) if ms is not None else None, info, st.ptr, B, H, Lq, Lk, D, float(scale), rq, rk)
+        return st
+
+
 # ------------------------------------------------------------------ backend
 
 class HipBackend:
@@ -431,6 +489,9 @@ class HipBackend:
                 self._call("layerNorm", "hb_layernorm", self.ctx, dtx, xp, ld, dtw, wp, bp, DT[lz.dt][0], st.ptr,
                            lz.rows, lz.D, lz.eps)
             lz.release()
+        elif isinstance(lz, _PendingSdpa):
+            t._st = lz.rowmajor().retain()  # t keeps its view (offset, strides) of the [B, Lq, H, D] output
+            lz.release()
         elif isinstance(lz, _PanelRows):
             st = self._malloc(_numel(t.shape) * DT[t.dtype][1])
             t._st, t._off, t._strides = st, 0, _contig(t.shape)
@@ -467,6 +528,12 @@ class HipBackend:
             self._call("layerNorm", "hb_layernorm_panel", self.ctx, dtx, xp, ld, dtw, wp, bp, st.ptr, lz.rows, lz.D,
                        lz.eps)
             x._lazy = _PanelRows(st, lz.rows, lz.D, norm=lz)  # keeps the LayerNorm's operands
+            return x._lazy
+        if (isinstance(lz, _PendingSdpa) and lz.panel_ok and x.shape[-1] == lz.K and x._off == 0
+                and tuple(x._strides) == _contig(x.shape) and _numel(x.shape[:-1]) == lz.M):
+            st = lz.panel()
+            lz.release()
+            x._lazy = _PanelRows(st, lz.M, lz.K)
             return x._lazy
         if (isinstance(lz, _PendingLinear) and lz.epi == F.HB_EPI_GEGLU and lz.arow_ok and lz.n_out % 64 == 0):
             M = lz.x[1]
@@ -674,6 +741,10 @@ class HipBackend:
             shape[shape.index(-1)] = n // known if known else 0
         if _numel(shape) != n:
             raise ValueError(f"reshape: cannot reshape [{','.join(map(str, x.shape))}] to [{','.join(map(str, shape))}]")
+        if isinstance(x._lazy, _PendingSdpa):  # a view of the pending output, not launched yet
+            st = self._nocopy_strides(x.shape, x._strides, shape)
+            if st is not None:
+                return self._track(HipTensor(shape, x.dtype, None, x._off, st, lazy=x._lazy.share()))
         self._ready(x)
         st = self._nocopy_strides(x.shape, x._strides, shape)
         if st is None:
@@ -739,6 +810,9 @@ class HipBackend:
         perm = [int(p) % len(x.shape) if len(x.shape) else 0 for p in perm]
         if sorted(perm) != list(range(len(x.shape))):
             raise ValueError(f"transpose: bad perm {perm} for rank {len(x.shape)}")
+        if isinstance(x._lazy, _PendingSdpa):  # a view of the pending output, not launched yet
+            return self._track(HipTensor([x.shape[p] for p in perm], x.dtype, None, x._off,
+                                         [x._strides[p] for p in perm], lazy=x._lazy.share()))
         self._ready(x)
         return self._view(x, [x.shape[p] for p in perm], [x._strides[p] for p in perm], x._off)
 
@@ -1156,17 +1230,17 @@ class HipBackend:
         return self._track(HipTensor(x.shape, dt, None, lazy=pend))
 
     def _attn_operand(self, t: HipTensor):
-        """(ptr, strides[4], rope_base) of a [B, H, L, D] sdpa operand."""
+        """(ptr, strides[4], rope_base, storage) of a [B, H, L, D] sdpa operand."""
         lz = t._lazy
         if isinstance(lz, _PendingRope) and lz.src[3] == t.dtype:
             st, off, strides, dtype, shape = lz.src
-            return st.ptr + off * DT[dtype][1], self._bhld_strides(shape, strides), lz.base
+            return st.ptr + off * DT[dtype][1], self._bhld_strides(shape, strides), lz.base, st
         self._ready(t)
         s = self._bhld_strides(t.shape, t._strides)
         if s is None:
             t = self._contiguous(t)
             s = self._bhld_strides(t.shape, t._strides)
-        return self._ptr(t), s, 0.0
+        return self._ptr(t), s, 0.0, t._st
 
     def sdpa(self, q: HipTensor, k: HipTensor, v: HipTensor, mask: Optional[HipTensor], scale: float) -> HipTensor:
         self._live(q, k, v, mask, op="sdpa")
@@ -1184,33 +1258,34 @@ class HipBackend:
             if t.dtype != dt:
                 t = self.cast(t, dt)
             ops.append(self._attn_operand(t))
-        (qp, qs, rq), (kp, ks, rk), (vp, vs, _) = ops
+        (qp, qs, rq, qst), (kp, ks, rk, kst), (vp, vs, _, vst) = ops
+        refs = [qst.retain(), kst.retain(), vst.retain()]
         mp, ms = 0, None
         mc = None
         if mask is not None:
             self._ready(mask)
             mc = mask if mask.dtype == "bool" else self.cast(mask, "bool")
             if len(mc.shape) > 4:
+                for r in refs:
+                    r.release()
                 raise ValueError("sdpa: mask rank > 4")
             full = (B, H, Lq, Lk)
             _broadcast_shape(mc.shape, full)
             ms = self._bstrides(mc, full)
             mp = self._ptr(mc)
+            refs.append(mc._st.retain())
         info = self._mask_info(mc, ms, B, Lq, Lk) if mc is not None else 0
-        # output physically [B, Lq, H, D], returned as a [B, H, Lq, D] view
-        st = self._malloc(B * Lq * H * D * DT[dt][1])
-        ostr = (Lq * H * D, D, H * D, 1)
-        out = self._track(HipTensor((B, H, Lq, D), dt, st, 0, ostr))
-        if B * H * Lq:
-            self.stats["sdpa"] += 1
-            if rq or rk:
-                self.stats["sdpa_fused_rope"] += 1
-            self._call("sdpa", "hb_sdpa", self.ctx, DT[dt][0], qp, F.i64s(qs), kp, F.i64s(ks), vp, F.i64s(vs), mp,
-                       F.i64s(ms) if ms is not None else None, info, st.ptr, F.i64s(ostr), B, H, Lq, Lk, D,
-                       float(scale), rq, rk)
+        # hb_sdpa_panel's conditions (its MFMA path), for a large-M consumer
+        panel_ok = (dt in ("f16", "bf16") and D == 64 and B * Lq >= PANEL_MIN_M and (H * D) % 64 == 0
+                    and all(p % 16 == 0 for p in (qp, kp, vp)) and all(st_[3] == 1 for st_ in (qs, ks, vs))
+                    and all(st_[i] % 8 == 0 for st_ in (qs, ks, vs) for i in range(3))
+                    and (ms is None or ms[1] == 0) and (Lk + 63) // 64 <= 1024)
+        args = (DT[dt][0], qp, qs, kp, ks, vp, vs, mp, ms, info, B, H, Lq, Lk, D, float(scale), rq, rk)
+        pend = _PendingSdpa(self, args, refs, panel_ok)
         if mc is not None and mc is not mask:
-            self.dispose(mc)
-        return out
+            self.dispose(mc)  # its storage is held by the pending launch
+        # output physically [B, Lq, H, D], returned as a [B, H, Lq, D] view
+        return self._track(HipTensor((B, H, Lq, D), dt, None, 0, (Lq * H * D, D, H * D, 1), lazy=pend))
 
     def _mask_info(self, mc: HipTensor, ms, B: int, Lq: int, Lk: int) -> int:
         """Device summary of a bool mask (per-tile: no / all / some keys

@@ -73,8 +73,8 @@ def test_sdpa_encoder_layout_config3(b, kind, dtype):
     mask = b.fromHost(mask_h)
     q, k, v = _qkv_views(b, dev, B, L, nh, hd)
     att = b.sdpa(b.rope(q, base), b.rope(k, base), v, mask, hd ** -0.5)
+    got = read32(b, att)  # [B, nh, L, hd]; the launch happens here, on first use
     assert b.stats["sdpa_fused_rope"] > 0
-    got = read32(b, att)  # [B, nh, L, hd]
     t = qkv.reshape(B, L, 3, nh, hd).transpose(2, 0, 3, 1, 4)
     tol = 5e-3 if dtype == "f16" else 2e-2
     for bb, hh in [(0, 0), (1, 5), (7, 11), (31, 3), (int(np.argmin(lens)), 7)]:

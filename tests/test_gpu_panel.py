@@ -168,3 +168,39 @@ def test_panel_quantized_bits(b, bits):
     np.testing.assert_array_equal(_bits(b, y_pan), _bits(b, y_row))
     C.dispose_quantized(b, Q)
     b.dispose(X)
+
+
+@pytest.mark.parametrize("window", [None, 128])
+def test_panel_attention_output_into_wo(b, window):
+    """The encoder's attention block (modernbert/src/index.ts:348-353): the
+    sdpa output stays pending through transpose + reshape, attn Wo reads it
+    in panel order (hb_sdpa_panel), bit for bit as with the row-major output,
+    with a padding mask (global) and a sliding-window mask."""
+    from laya_hip.modernbert import attentionMasks
+    B, L, nh, hd = 8, 512, 12, 64
+    H = nh * hd
+    rng = np.random.default_rng(11)
+    lens = rng.integers(64, L + 1, B)
+    valid = (np.arange(L)[None, :] < lens[:, None]).astype(np.uint8)
+    full, sliding = attentionMasks(valid, B, L, 128)
+    mask = b.fromHost(full if window is None else sliding)
+    qkv = b.fromHost(to_host(rounded(rng.standard_normal((B, L, 3 * H)), "f16"), "f16"))
+    Wo = b.fromHost(to_host(rounded(rng.normal(0, 0.02, (H, H)), "f16"), "f16"))
+    R = b.fromHost(to_host(rounded(rng.standard_normal((B, L, H)), "f16"), "f16"))
+
+    def block(materialize):
+        t = b.transpose(b.reshape(qkv, [B, L, 3, nh, hd]), [2, 0, 3, 1, 4])
+        q, k, v = [b.reshape(x, [B, nh, L, hd]) for x in b.split(t, 3, 0)]
+        att = b.sdpa(b.rope(q, 1e4), b.rope(k, 1e4), v, mask, hd ** -0.5)
+        if materialize:
+            b._ready(att)
+        merged = b.reshape(b.transpose(att, [0, 2, 1, 3]), [B, L, H])
+        y = b.add(R, b.linear(merged, Wo))
+        if not materialize:
+            assert isinstance(merged._lazy, _PanelRows)
+        return _bits(b, y), _bits(b, att)
+
+    pan, pan_att = block(False)
+    row, row_att = block(True)
+    np.testing.assert_array_equal(pan, row)
+    np.testing.assert_array_equal(pan_att, row_att)  # the pending output read on its own, row-major
