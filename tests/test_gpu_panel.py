@@ -204,3 +204,47 @@ def test_panel_attention_output_into_wo(b, window):
     row, row_att = block(True)
     np.testing.assert_array_equal(pan, row)
     np.testing.assert_array_equal(pan_att, row_att)  # the pending output read on its own, row-major
+
+
+def test_encoder_forwards_release_every_block(b):
+    """Pending layerNorm / sdpa / geglu tensors, their shared views and panel
+    copies are all freed: repeated forwards of a 3-layer encoder at M = 4096
+    (every panel path taken) leave the pool's live block count unchanged, and
+    so does a forward whose intermediate is read half-way."""
+    from laya_hip.modernbert import loadModernBert, parseModernBertConfig
+    H, I, NH, V, B, T = 768, 1152, 12, 1000, 8, 512
+    cfgj = {"vocab_size": V, "hidden_size": H, "intermediate_size": I, "num_hidden_layers": 3,
+            "num_attention_heads": NH, "local_attention": 128}
+    rng = np.random.default_rng(12)
+    n = lambda *s: (rng.standard_normal(s, dtype=np.float32) * 0.02).astype(np.float16)  # noqa: E731
+    W = {"embeddings.tok_embeddings.weight": n(V, H), "embeddings.norm.weight": np.ones(H, np.float16),
+         "final_norm.weight": np.ones(H, np.float16)}
+    for i in range(3):
+        p = f"layers.{i}."
+        if i:
+            W[p + "attn_norm.weight"] = np.ones(H, np.float16)
+        W.update({p + "attn.Wqkv.weight": n(3 * H, H), p + "attn.Wo.weight": n(H, H),
+                  p + "mlp_norm.weight": np.ones(H, np.float16), p + "mlp.Wi.weight": n(2 * I, H),
+                  p + "mlp.Wo.weight": n(H, I)})
+    enc = loadModernBert(b, parseModernBertConfig(cfgj),
+                         lambda nm: HostTensor("f16", W[nm[8:]].shape, W[nm[8:]]) if nm[8:] in W else None,
+                         dtype="f16")
+    lens = rng.integers(64, T + 1, B)
+    ids = rng.integers(0, V, (B, T)).astype(np.int32)
+    valid = (np.arange(T)[None, :] < lens[:, None]).astype(np.uint8)
+    inp = enc.uploadInputs(ids, valid, B, T)
+    first = _bits(b, enc.encode(inp))  # the mask summaries are built (and cached) here
+    before = b.pool_stats()["live_blocks"]
+    for _ in range(2):
+        b.dispose(enc.encode(inp))
+        assert b.pool_stats()["live_blocks"] == before
+    x = b.scope(lambda: enc.embeddings(inp["ids"]))
+    h = enc.layer(0, x, inp["masks"]["full_attention"])
+    mid = _bits(b, h)  # an intermediate read in the middle of the pending chain
+    assert np.isfinite(mid.view(np.float16).astype(np.float32)).all()
+    for t in (x, h):
+        b.dispose(t)
+    assert b.pool_stats()["live_blocks"] == before
+    np.testing.assert_array_equal(_bits(b, enc.encode(inp)), first)  # and the result is unchanged
+    enc.disposeInputs(inp)
+    enc.dispose()
