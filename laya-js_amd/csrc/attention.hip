@@ -2,19 +2,23 @@
 //
 // sdpa_mfma: flash attention for head dim 64 in fp16 / bf16 on
 // v_mfma_f32_16x16x32.  A block owns 128 queries of one (b, h); each of its
-// four waves owns 32 of them.  Per 64-key tile the wave computes
+// eight waves owns 16 of them.  Per 64-key tile the wave computes
 // S^T = K . Q^T, so a lane ends up holding the scores of ONE query for 8
-// keys -- exactly the B-operand layout of O^T = V^T . P^T, so P never leaves
-// registers.  The rows of K are fed to the MFMA in a permuted order that
-// makes those 8 keys contiguous, which lets the lane read its 8 mask bytes
-// with one load and its V^T fragment (V transposed in LDS) with one 16-byte
-// read.  Softmax is online, in f32, in the log2 domain.  Key tiles outside
-// the range where the (b, query tile) mask has any visible key are skipped:
-// a pre-pass over the bool mask finds that range, so the sliding-window
-// layers touch only the tiles inside the window (plus the full rows of
-// padded queries, which see every valid key).  RoPE, when fused, rotates the
-// Q and K tiles as they are staged and rounds them to the storage type,
-// bit-identical to a separate Backend.rope.
+// contiguous keys per 32-key half -- exactly the B-operand layout of
+// O^T = V^T . P^T, so P never leaves registers.  The rows of K are fed to the
+// MFMA in a permuted order that makes those 8 keys contiguous, which lets the
+// lane read its 8 mask bytes with one load and its V^T fragment (V transposed
+// in LDS) with one 16-byte read.  K and V^T tiles are double-buffered in LDS,
+// loaded into registers two tiles ahead (waves 0-3 fetch K, waves 4-7 V).
+// Softmax is online, in f32, in the log2 domain.  A pre-pass over the bool
+// mask classes every (b, query tile, key tile, 16-query group) as skipped,
+// all visible or masked: tiles no group needs are never staged, and a group
+// skips the tiles it cannot see, so the sliding-window layers touch only the
+// tiles inside the window (plus the full rows of padded queries, which see
+// every valid key).  RoPE, when fused, rotates the Q and K tiles as they are
+// staged and rounds them to the storage type, bit-identical to a separate
+// Backend.rope.  The output is written row-major or, for the attention output
+// projection, in the panel order of the GEMM's X operand.
 //
 // sdpa_simt: the f32 path and the fallback for other head dims / layouts.
 #include <stdexcept>
@@ -286,8 +290,8 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
     }
   };
 
-  // this lane's mask bytes of a tile: 8 contiguous keys for each of its two
-  // queries (qb) and halves (t)
+  // this lane's mask bytes of a tile: 8 contiguous keys of its query (one per
+  // 16-query block qb) in each 32-key half t
   auto load_mask = [&](int kt, uint2v (&mw)[kQB][2]) {
     const int k0 = kt * kBK;
 #pragma unroll

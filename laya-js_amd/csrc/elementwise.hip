@@ -1,5 +1,6 @@
 // Bandwidth kernels: strided copy/cast and elementwise math, broadcasting
-// binary ops, where, GeGLU, gathers, masked mean pooling, fills.
+// binary ops, where, GeGLU, gathers, masked mean pooling, fills, and the
+// row-major <-> panel-order repacking of 16-bit matrices.
 #include <stdexcept>
 
 #include "common.h"

@@ -5,8 +5,12 @@
 // Two MFMA kernels, both on gfx950's v_mfma_f32_32x32x16_{f16,bf16} with the
 // same operand order (W rows as the A operand, X rows as the B operand) and
 // the same sequence of k16 steps, so a row's output bits do not depend on M:
-// - gemm_mfma_arow (M >= 4096): persistent, 256 x 192 tiles, X rows in
-//   registers, W tiles double-buffered in LDS, epilogue from registers;
+// - gemm_mfma_arow (M >= 4096): persistent, 256 x 192 tiles, one wave per
+//   SIMD; X rows in registers (loaded two stages ahead), W tiles
+//   double-buffered in LDS; the output (and the residual, fetched into the
+//   same LDS C tile) is staged in LDS and written during the first stages of
+//   the block's next tile.  X and Y may be row-major or in panel order
+//   (32-row x 16-column blocks of 1 KB laid out as MFMA operands);
 // - gemm_mfma (smaller M): 128 x 128 tiles, A and B double-buffered in LDS,
 //   epilogue staged in LDS and written with 16-byte stores.
 // Both take 64-wide K stages of 16-byte chunks XOR-swizzled by row so the

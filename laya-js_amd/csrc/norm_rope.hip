@@ -1,4 +1,5 @@
-// LayerNorm (wave-per-row, f32 two-pass statistics) and split-half RoPE.
+// LayerNorm (wave-per-row, f32 two-pass statistics; written row-major or in
+// the panel order of the GEMM's X operand) and split-half RoPE.
 #include <stdexcept>
 #include <type_traits>
 
