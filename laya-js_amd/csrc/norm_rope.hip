@@ -95,32 +95,34 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(const uint16_t* __re
   for (int g = 0; g < G; g++) *(uint2v*)(yr + (g * 64 + lane) * 4) = out[g];
 }
 
-// Panel-order output: a block of 256 threads normalises 8 consecutive rows
-// (2 per wave, loads issued first).  In panel order those rows' chunks of one
-// (16-column block, half) pair form one 128-byte line, so the block stages
-// its rows in LDS line by line -- chunk of row i in line l at slot
-// (i + l) % 8, which spreads a wave's writes over the banks -- and writes
+// Panel-order output: a block of 512 threads normalises 8 consecutive rows,
+// one per wave (two per wave in 256-thread blocks measured 6% slower: a
+// wave's normalisations run one after the other).  In panel order those
+// rows' chunks of one (16-column block, half) pair form one 128-byte line, so
+// the block stages its rows in LDS line by line -- chunk of row i in line l at
+// slot (i + l) % 8, which spreads a wave's writes over the banks -- and writes
 // each line whole with 8 consecutive 16-byte stores.  The grid covers the
 // padding rows of the last 32-row block, which are written as zeros.
+constexpr int kLnRpw = 1, kLnNT = 64 * 8 / kLnRpw;  // rows per wave, threads per block (8 rows)
 template <int G, bool BF, int PK>
-__global__ __launch_bounds__(256) void layernorm_panel_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+__global__ __launch_bounds__(kLnNT) void layernorm_panel_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                               const void* __restrict__ w, const void* __restrict__ b,
                                                               uint16_t* __restrict__ y, int64_t rows, int D,
                                                               float eps) {
   extern __shared__ __attribute__((aligned(16))) uint16_t tile[];  // [D / 8 lines][8 slots][8]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row0 = (int64_t)blockIdx.x * 8;
-  uint2v raw[2][G];
+  uint2v raw[kLnRpw][G];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int64_t row = row0 + wave * 2 + i;
+  for (int i = 0; i < kLnRpw; i++) {
+    const int64_t row = row0 + wave * kLnRpw + i;
     const uint16_t* xr = x + (row < rows ? row : rows - 1) * ldx;
 #pragma unroll
     for (int g = 0; g < G; g++) raw[i][g] = *(const uint2v*)(xr + (g * 64 + lane) * 4);
   }
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int r = wave * 2 + i;
+  for (int i = 0; i < kLnRpw; i++) {
+    const int r = wave * kLnRpw + i;
     uint2v out[G];
     if (row0 + r < rows) {
       ln_row<G, BF, PK>(raw[i], lane, w, b, D, eps, out);
@@ -137,7 +139,7 @@ __global__ __launch_bounds__(256) void layernorm_panel_kernel(const uint16_t* __
   __syncthreads();
   const int64_t kb = D >> 4;  // 16-column blocks per row
   uint16_t* yb = y + (row0 >> 5) * kb * 512;
-  for (int q = threadIdx.x; q < D; q += 256) {
+  for (int q = threadIdx.x; q < D; q += kLnNT) {
     const int l = q >> 3, sl = q & 7, i = (sl - l) & 7;
     const int r32 = (int)(row0 & 31) + i;
     *(uint4v*)(yb + (int64_t)(l >> 1) * 512 + ((l & 1) * 32 + r32) * 8) = *(const uint4v*)(tile + q * 8);
@@ -220,8 +222,8 @@ static void launch_ln16(bool panel, hipStream_t st, bool bf, int pk, const uint1
         attr = true;
       }
       auto kern = bf ? layernorm_panel_kernel<GG, true, PP> : layernorm_panel_kernel<GG, false, PP>;
-      kern<<<(unsigned)((rows + 31) / 32 * 4), 256, lds, st>>>(x, ldx, (const void*)w, (const void*)b, y, rows, D,
-                                                                eps);
+      kern<<<(unsigned)((rows + 31) / 32 * 4), kLnNT, lds, st>>>(x, ldx, (const void*)w, (const void*)b, y, rows, D,
+                                                                  eps);
     } else {
       auto kern = bf ? layernorm_vec_kernel<GG, true, PP> : layernorm_vec_kernel<GG, false, PP>;
       kern<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(x, ldx, (const void*)w, (const void*)b, y, rows, D, eps);
