@@ -77,8 +77,12 @@ def test_panel_entry_points_reject_unsupported_calls(b):
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("pdt", [None, "same", "f32"])
-def test_layernorm_panel_bits(b, dtype, pdt):
-    M, D = 4100, 768
+@pytest.mark.parametrize("D", [768, 256, 1024, 2048])
+def test_layernorm_panel_bits(b, dtype, pdt, D):
+    """Panel-order LayerNorm = row-major LayerNorm bit for bit, for row widths
+    of every register-group count the kernel is built for (D / 256 = 1, 3, 4,
+    8) and a last 8-row block that is only half full (M = 4100)."""
+    M = 4100
     rng = np.random.default_rng(3)
     x = rounded(rng.standard_normal((M, D)) * 2 + 0.5, dtype)
     X = b.fromHost(to_host(x, dtype))
