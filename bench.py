@@ -349,8 +349,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the encoder is "
-              "data-parallel over sequences and would shard by batch rows with no collectives -- see DESIGN.md",
-              file=sys.stderr)
+              "data-parallel over sequences: N GPUs would each encode B/N of the batch rows with the same "
+              "weights, with no collective on the path", file=sys.stderr)
         sys.exit(2)
     if args.mode == "gemm":
         run_gemm_sweep(args)
