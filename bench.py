@@ -24,6 +24,7 @@ Prints ONE JSON line on stdout.  `value` comes from a clean timed region
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
   python bench.py --mode gemm    # isolated config-1/2 GEMM sweep (stderr table + JSON lines)
   python bench.py --mode copy    # the library's contiguous copy kernel (HBM counter calibration)
+  python bench.py --mode config4 # BASELINE config 4 (ModernBERT-large shape, B=16, T=2048), fp16 and quantized
 """
 from __future__ import annotations
 
@@ -230,6 +231,99 @@ def run_encode(args) -> dict:
     return res
 
 
+LARGE = {"vocab_size": 256000, "hidden_size": 1024, "intermediate_size": 2624, "num_hidden_layers": 28,
+         "num_attention_heads": 16, "local_attention": 128}
+
+
+def run_config4(args) -> None:
+    """the ModernBERT-large-shape encoder (hidden 1024, 28
+    layers, 16 heads, GeGLU 2624, window 128 / global every third layer,
+    256000-token vocabulary) at B = 16, T = 2048 (full-length sequences),
+    then the pooled 1024 -> 8 classifier with softmax; fp16 weights, then
+    laya's quantized format (q4 affine Linears, group 64, and a q8 symmetric
+    embedding table).  The quantized codes, scales and zeros are drawn at
+    random in the format's ranges (the kernels' time does not depend on the
+    values; tests/test_gpu_config4.py checks the numerics).  One JSON line
+    per weight format."""
+    from laya_hip.backend import HipBackend
+    from laya_hip.compose import mean_pool
+    from laya_hip.host import HostQuantized, HostTensor, pack_quantized
+    from laya_hip.modernbert import loadModernBert, parseModernBertConfig
+
+    B, T, C = 16, 2048, 8
+    H, I, V = LARGE["hidden_size"], LARGE["intermediate_size"], LARGE["vocab_size"]
+    cfg = parseModernBertConfig(LARGE)
+    rng = np.random.default_rng(4)
+    ids = rng.integers(0, V, (B, T)).astype(np.int32)
+    valid = np.ones((B, T), np.uint8)
+    be = HipBackend(0)
+    Wc = be.fromHost(HostTensor("f32", (C, H), (rng.standard_normal((C, H)) * 0.5).astype(np.float32)))
+    bc = be.fromHost(HostTensor("f32", (C,), (rng.standard_normal(C) * 0.1).astype(np.float32)))
+    t0 = time.time()
+    W = make_weights(LARGE, seed=4)
+    log(f"config4: fp16 weights generated in {time.time() - t0:.1f}s")
+
+    def quantized(name):
+        v = W[name]
+        N, K = v.shape
+        if name == "embeddings.tok_embeddings.weight":
+            q = rng.integers(-127, 128, (N, K), dtype=np.int64)
+            s = rng.uniform(1e-4, 3e-4, (N, K // 64)).astype(np.float16)
+            return HostQuantized((N, K), 8, 64, "symmetric", pack_quantized(q, 8), HostTensor("f16", s.shape, s), None)
+        q = rng.integers(0, 16, (N, K), dtype=np.int64)
+        s = rng.uniform(2e-3, 6e-3, (N, K // 64)).astype(np.float16)
+        z = (-7.5 * s.astype(np.float32)).astype(np.float16)
+        return HostQuantized((N, K), 4, 64, "affine", pack_quantized(q, 4), HostTensor("f16", s.shape, s),
+                             HostTensor("f16", z.shape, z))
+
+    def getter(fmt):
+        def get(nm):
+            if not nm.startswith("encoder.") or nm[8:] not in W:
+                return None
+            k = nm[8:]
+            if fmt == "quantized" and (k.endswith(("Wqkv.weight", "Wo.weight", "Wi.weight")) or
+                                        k == "embeddings.tok_embeddings.weight"):
+                return quantized(k)
+            return HostTensor("f16", W[k].shape, W[k])
+        return get
+
+    for fmt in ("fp16", "quantized"):
+        t0 = time.time()
+        enc = loadModernBert(be, cfg, getter(fmt), dtype="f16")
+        inp = enc.uploadInputs(ids, valid, B, T)
+        be.flush()
+        log(f"config4 {fmt}: weights + inputs resident in {time.time() - t0:.1f}s")
+
+        def step():
+            def f():
+                pooled = mean_pool(be, enc.encode(inp), inp["mask"])
+                return be.softmax(be.linear(pooled, Wc, bc), -1)
+            return be.scope(f)
+
+        for _ in range(args.warmup):
+            be.dispose(step())
+        ev0, ev1 = be.event(), be.event()
+        be.flush()
+        be.record(ev0)
+        for _ in range(args.steps):
+            be.dispose(step())
+        be.record(ev1)
+        be.flush()
+        ms = be.elapsed_ms(ev0, ev1) / args.steps
+        print(json.dumps({"mode": "config4", "metric": "ModernBERT-large encode + pooled classifier tokens/s at "
+                          "B=16,T=2048", "weights": fmt, "value": B * T / (ms * 1e-3), "unit": "tokens/s",
+                          "ms_per_step": ms, "steps": args.steps, "warmup": args.warmup, "dtype": "f16",
+                          "data": "synthetic (random-init weights, ids U[0,256000), full-length sequences)",
+                          "config": {"workload": "BASELINE config 4", "global_batch": B, "seq_len": T,
+                                     "layers": LARGE["num_hidden_layers"], "hidden": H, "intermediate": I,
+                                     "vocab": V}}), flush=True)
+        enc.disposeInputs(inp)
+        enc.dispose()
+    be.dispose(Wc)
+    be.dispose(bc)
+    be.destroy()
+
+
 def cpu_baseline(sample_b: int = 8) -> dict:
     """The CPU oracle (C, OpenMP, f64 accumulation) on `sample_b` of the 32
     sequences at T=512, all 22 layers; reported as tokens/s of that sample."""
@@ -342,7 +436,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--mode", choices=["encode", "gemm", "copy"], default="encode")
+    ap.add_argument("--mode", choices=["encode", "gemm", "copy", "config4"], default="encode")
     ap.add_argument("--copy-mib", type=int, default=512, help="buffer size for --mode copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-sample", type=int, default=8, help="sequences in the CPU-baseline sample")
@@ -352,6 +446,9 @@ def main():
               "data-parallel over sequences: N GPUs would each encode B/N of the batch rows with the same "
               "weights, with no collective on the path", file=sys.stderr)
         sys.exit(2)
+    if args.mode == "config4":
+        run_config4(args)
+        return
     if args.mode == "gemm":
         run_gemm_sweep(args)
         return

@@ -232,6 +232,66 @@ __global__ void meanpool_kernel(int dt_x, const void* __restrict__ x, const uint
   }
 }
 
+// 16-bit x, D % 8 == 0: two passes.  meanpool16_partial: block (column chunk
+// of 512, row slice s of S, batch row b); thread t sums columns 8 (t % 64)
+// .. + 7 of the chunk over the slice's rows l = l0 + t / 64 (mod 4), with
+// 16-byte loads; the four row groups are added in LDS in a fixed order.
+// meanpool16_final adds the S slice sums in order and divides by the
+// count of visible rows.  Same result on every run (no atomics).
+template <bool BF>
+__global__ __launch_bounds__(256) void meanpool16_partial(const uint16_t* __restrict__ x,
+                                                          const uint8_t* __restrict__ mask, int64_t B, int64_t L,
+                                                          int64_t D, int S, float* __restrict__ part,
+                                                          float* __restrict__ cnt) {
+  __shared__ float red[4][512];
+  __shared__ float redn[4];
+  const int c = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t b = blockIdx.z, s = blockIdx.y, d = (int64_t)blockIdx.x * 512 + c * 8;
+  const int64_t l0 = L * s / S, l1 = L * (s + 1) / S;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float n = 0.f;
+  const bool dok = d < D;
+  const uint16_t* xb = x + b * L * D + (dok ? d : 0);
+  const uint8_t* mb = mask + b * L;
+#pragma unroll 4
+  for (int64_t l = l0 + g; l < l1; l += 4) {
+    const uint4v v = *(const uint4v*)(xb + l * D);
+    const bool vis = mb[l] != 0;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float lo = BF ? bf16_to_f32((uint16_t)(w[e] & 0xffff)) : f16_bits_to_f32((uint16_t)(w[e] & 0xffff));
+      const float hi = BF ? bf16_to_f32((uint16_t)(w[e] >> 16)) : f16_bits_to_f32((uint16_t)(w[e] >> 16));
+      acc[2 * e] += vis ? lo : 0.f;
+      acc[2 * e + 1] += vis ? hi : 0.f;
+    }
+    n += vis ? 1.f : 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) red[g][c * 8 + e] = acc[e];
+  if (c == 0) redn[g] = n;
+  __syncthreads();
+  if (g == 0 && dok) {
+    float* pp = part + (s * B + b) * D + d;
+#pragma unroll
+    for (int e = 0; e < 8; e++) pp[e] = ((red[0][c * 8 + e] + red[1][c * 8 + e]) + red[2][c * 8 + e]) + red[3][c * 8 + e];
+  }
+  if (threadIdx.x == 0 && blockIdx.x == 0) cnt[s * B + b] = ((redn[0] + redn[1]) + redn[2]) + redn[3];
+}
+
+__global__ void meanpool16_final(const float* __restrict__ part, const float* __restrict__ cnt, int64_t B, int64_t D,
+                                 int S, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * D) return;
+  const int64_t b = i / D;
+  float sum = 0.f, n = 0.f;
+  for (int s = 0; s < S; s++) {
+    sum += part[s * B * D + i];
+    n += cnt[s * B + b];
+  }
+  out[i] = sum / fmaxf(n, 1.0f);
+}
+
 // Index of the first maximum (minimum) of x[base + j * inner], j < n; a NaN
 // counts as the extremum (numpy's rule).
 __device__ __noinline__ int32_t argreduce(bool is_max, int dt_x, const void* __restrict__ x, int64_t base, int64_t n,
@@ -514,8 +574,30 @@ int hb_meanpool(uintptr_t ctx, int dt_x, uintptr_t x, uintptr_t mask, int64_t B,
   HB_API_BEGIN
   int64_t total = B * D;
   if (total == 0) return 0;
-  meanpool_kernel<<<grid_for(total, 256), 256, 0, stream_of(ctx)>>>(dt_x, (const void*)x, (const uint8_t*)mask, B,
-                                                                     L, D, (float*)out);
+  hipStream_t st = stream_of(ctx);
+  if ((dt_x == HB_F16 || dt_x == HB_BF16) && D % 8 == 0 && x % 16 == 0 && L > 0 && B <= 65535) {
+    // row slices: enough blocks to fill the device, at least 16 rows each
+    const int64_t chunks = (D + 511) / 512;
+    int64_t S = (4 * 256 + B * chunks - 1) / (B * chunks);
+    S = S < 1 ? 1 : (S > 64 ? 64 : S);
+    if (S > (L + 15) / 16) S = (L + 15) / 16;
+    if (S < 1) S = 1;
+    float* part = (float*)pool_alloc(ctx, (size_t)(S * B * D + S * B) * sizeof(float));
+    float* cnt = part + S * B * D;
+    dim3 grid((unsigned)chunks, (unsigned)S, (unsigned)B);
+    if (dt_x == HB_BF16)
+      meanpool16_partial<true><<<grid, 256, 0, st>>>((const uint16_t*)x, (const uint8_t*)mask, B, L, D, (int)S, part,
+                                                     cnt);
+    else
+      meanpool16_partial<false><<<grid, 256, 0, st>>>((const uint16_t*)x, (const uint8_t*)mask, B, L, D, (int)S,
+                                                      part, cnt);
+    meanpool16_final<<<grid_for(total, 256), 256, 0, st>>>(part, cnt, B, D, (int)S, (float*)out);
+    check_launch("hb_meanpool");
+    pool_free(ctx, part);
+    return 0;
+  }
+  meanpool_kernel<<<grid_for(total, 256), 256, 0, st>>>(dt_x, (const void*)x, (const uint8_t*)mask, B, L, D,
+                                                        (float*)out);
   check_launch("hb_meanpool");
   HB_API_END
 }
