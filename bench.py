@@ -25,6 +25,7 @@ Prints ONE JSON line on stdout.  `value` comes from a clean timed region
   python bench.py --mode gemm    # isolated config-1/2 GEMM sweep (stderr table + JSON lines)
   python bench.py --mode copy    # the library's contiguous copy kernel (HBM counter calibration)
   python bench.py --mode config4 # BASELINE config 4 (ModernBERT-large shape, B=16, T=2048), fp16 and quantized
+  python bench.py --mode config0 # BASELINE config 0 (B=1, T=128): ms per forward, CPU oracle beside it
 """
 from __future__ import annotations
 
@@ -324,6 +325,54 @@ def run_config4(args) -> None:
     be.destroy()
 
 
+def run_config0(args) -> None:
+    """the ModernBERT-base-shape encoder at batch 1, seq
+    128, no padding (the reference's CPU-runnable case): GPU ms per forward
+    (inputs resident), with the CPU oracle timed on the same forward."""
+    from laya_hip.backend import HipBackend
+    from laya_hip.host import HostTensor
+    from laya_hip.modernbert import loadModernBert, parseModernBertConfig
+    from oracle import cpu_ref as cr
+
+    B, T = 1, 128
+    cfg = parseModernBertConfig(BASE)
+    W = make_weights(BASE)
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, BASE["vocab_size"], (B, T)).astype(np.int32)
+    valid = np.ones((B, T), np.uint8)
+    be = HipBackend(0)
+    enc = loadModernBert(be, cfg, lambda nm: HostTensor("f16", W[nm[8:]].shape, W[nm[8:]])
+                         if nm.startswith("encoder.") and nm[8:] in W else None, dtype="f16")
+    inp = enc.uploadInputs(ids, valid, B, T)
+    for _ in range(args.warmup):
+        be.dispose(enc.encode(inp))
+    ev0, ev1 = be.event(), be.event()
+    be.flush()
+    be.record(ev0)
+    for _ in range(args.steps):
+        be.dispose(enc.encode(inp))
+    be.record(ev1)
+    be.flush()
+    ms = be.elapsed_ms(ev0, ev1) / args.steps
+    enc.disposeInputs(inp)
+    enc.dispose()
+    be.destroy()
+    cfg0 = cr.EncoderConfig.from_json(BASE)
+    W32 = {k: v.astype(np.float32) for k, v in W.items()}
+    t0 = time.perf_counter()
+    y = cr.encoder_forward(cfg0, W32, ids, valid)
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    assert np.isfinite(y).all()
+    print(json.dumps({"mode": "config0", "metric": "ModernBERT-base encode ms per forward at B=1,T=128",
+                      "value": ms, "unit": "ms", "higher_is_better": False, "tokens_per_s": B * T / (ms * 1e-3),
+                      "steps": args.steps, "warmup": args.warmup, "dtype": "f16",
+                      "data": "synthetic (random-init fp16 weights ~N(0,0.02), ids U[0,50368), no padding)",
+                      "config": {"workload": "BASELINE config 0", "global_batch": B, "seq_len": T},
+                      "cpu_baseline": {"value": cpu_ms, "unit": "ms", "cores": cr.num_threads(), "kind": "port",
+                                       "sample": "the same forward on the CPU oracle (f32 storage, f64 "
+                                                 "accumulation)"}}), flush=True)
+
+
 def cpu_baseline(sample_b: int = 8) -> dict:
     """The CPU oracle (C, OpenMP, f64 accumulation) on `sample_b` of the 32
     sequences at T=512, all 22 layers; reported as tokens/s of that sample."""
@@ -436,7 +485,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--mode", choices=["encode", "gemm", "copy", "config4"], default="encode")
+    ap.add_argument("--mode", choices=["encode", "gemm", "copy", "config0", "config4"], default="encode")
     ap.add_argument("--copy-mib", type=int, default=512, help="buffer size for --mode copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-sample", type=int, default=8, help="sequences in the CPU-baseline sample")
@@ -448,6 +497,9 @@ def main():
         sys.exit(2)
     if args.mode == "config4":
         run_config4(args)
+        return
+    if args.mode == "config0":
+        run_config0(args)
         return
     if args.mode == "gemm":
         run_gemm_sweep(args)
