@@ -113,7 +113,7 @@ class _Storage:
             for p in self.cache.values():  # device summaries derived from this storage
                 self.owner._free(p)
             self.cache.clear()
-            self.owner._free(self.ptr)
+            self.owner._recycle(self.ptr, self.nbytes)
             self.ptr = 0
 
 
@@ -380,6 +380,7 @@ class HipBackend:
         self._profiling = None  # list of (key, start event, end event) while profiling
         self._prof_only = self._LAUNCHES
         self._event_pool: list[int] = []
+        self._blocks: dict[int, list[int]] = {}
         self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "sdpa": 0,
                       "sdpa_fused_rope": 0, "copies": 0, "panel_unpacks": 0}
 
@@ -436,12 +437,46 @@ class HipBackend:
         self._call("deviceInfo", "hb_device_info", self.ctx, buf, 1024)
         return json.loads(buf.value.decode())
 
+    # Blocks of disposed tensors wait in `_blocks` (size class -> pointers)
+    # for the next allocation of the same class, without a call into the
+    # library either way.  The library's pool is stream-ordered on the one
+    # stream, and so is this: a block handed out again is only written by
+    # work queued after everything that read it.  The size classes are the
+    # library's (runtime.hip, size_class).
+    @staticmethod
+    def _size_class(nbytes: int) -> int:
+        n = max(1, nbytes)
+        if n <= 65536:
+            return (n + 255) & ~255
+        step = (1 << (n - 1).bit_length()) // 16
+        return (n + step - 1) // step * step
+
     def _malloc(self, nbytes: int) -> _Storage:
         if self._destroyed:
             raise RuntimeError("hip backend: used after destroy()")
+        sc = self._size_class(nbytes)
+        free = self._blocks.get(sc)
+        if free:
+            return _Storage(self, free.pop(), nbytes)
         p = F.U(0)
-        self._call("alloc", "hb_alloc", self.ctx, max(1, nbytes), F.C.byref(p))
+        try:
+            self._call("alloc", "hb_alloc", self.ctx, sc, F.C.byref(p))
+        except RuntimeError:
+            if not any(self._blocks.values()):
+                raise
+            self._return_blocks()  # hand the waiting blocks back to the library and retry once
+            self._call("alloc", "hb_alloc", self.ctx, sc, F.C.byref(p))
         return _Storage(self, p.value, nbytes)
+
+    def _recycle(self, ptr: int, nbytes: int):
+        if not self._destroyed:
+            self._blocks.setdefault(self._size_class(nbytes), []).append(ptr)
+
+    def _return_blocks(self):
+        for ptrs in self._blocks.values():
+            for ptr in ptrs:
+                self._free(ptr)
+        self._blocks.clear()
 
     def _free(self, ptr: int):
         if not self._destroyed:
@@ -721,10 +756,12 @@ class HipBackend:
 
     def destroy(self) -> None:
         if not self._destroyed:
+            self._blocks.clear()  # the library frees every block with the context
             self._call("destroy", "hb_destroy", self.ctx)
             self._destroyed = True
 
     def pool_stats(self) -> dict:
+        self._return_blocks()  # blocks waiting for reuse count as cached, not live
         a, b, c = F.U(0), F.U(0), F.U(0)
         self._call("poolStats", "hb_pool_stats", self.ctx, F.C.byref(a), F.C.byref(b), F.C.byref(c))
         return {"live_bytes": a.value, "cached_bytes": b.value, "live_blocks": c.value}
