@@ -101,7 +101,7 @@ class _Storage:
         self.ptr = ptr
         self.nbytes = nbytes
         self.refs = 1
-        self.cache: dict = {}
+        self.cache: Optional[dict] = None  # device summaries derived from this storage, created on first use
 
     def retain(self):
         self.refs += 1
@@ -110,9 +110,10 @@ class _Storage:
     def release(self):
         self.refs -= 1
         if self.refs == 0 and self.ptr:
-            for p in self.cache.values():  # device summaries derived from this storage
-                self.owner._free(p)
-            self.cache.clear()
+            if self.cache:
+                for p in self.cache.values():
+                    self.owner._free(p)
+            self.cache = None
             self.owner._recycle(self.ptr, self.nbytes)
             self.ptr = 0
 
@@ -122,14 +123,14 @@ class HipTensor:
     __slots__ = ("shape", "dtype", "_st", "_off", "_strides", "_lazy", "_dead", "_meta", "__weakref__")
 
     def __init__(self, shape, dtype, st: Optional[_Storage], off: int = 0, strides=None, lazy=None):
-        self.shape = tuple(int(d) for d in shape)
+        self.shape = tuple(map(int, shape))
         self.dtype = dtype
         self._st = st
         self._off = off
         self._strides = tuple(strides) if strides is not None else _contig(self.shape)
         self._lazy = lazy
         self._dead = False
-        self._meta: dict = {}
+        self._meta: Optional[dict] = None  # created on first use
 
     @property
     def size(self) -> int:
@@ -707,10 +708,10 @@ class HipBackend:
         if t._st is not None:
             t._st.release()
             t._st = None
-        for k, v in list(t._meta.items()):
+        for k, v in list((t._meta or {}).items()):
             if isinstance(v, HipTensor):
                 self.dispose(v)
-        t._meta.clear()
+        t._meta = None
 
     def scope(self, fn: Callable[[], Any]):
         """index.ts:158-162: tensors created inside `fn` and not returned
@@ -1331,6 +1332,8 @@ class HipBackend:
         if ms[1] != 0 or not (B and Lq and Lk):
             return 0
         key = ("sdpa_tiles", mc._off, tuple(ms), B, Lq, Lk)
+        if mc._st.cache is None:
+            mc._st.cache = {}
         cache = mc._st.cache
         if key not in cache:
             n = F.C.c_size_t(0)
@@ -1394,6 +1397,8 @@ class HipBackend:
         w = self.fromHost(HostTensor("u8", (N, K * h.bits // 8), np.asarray(h.data, np.uint8).reshape(N, -1)))
         sc = self.fromHost(HostTensor("f16", (N, G), s16.reshape(N, G)))
         zb = self.fromHost(HostTensor("f16", (N, G), z16.reshape(N, G))) if z16 is not None else None
+        if sc._meta is None:
+            sc._meta = {}
         sc._meta["deq_dtype"] = dtype
         return QuantizedTensor((N, K), h.bits, h.groupSize, h.mode, dtype, True, w, sc, zb)
 
@@ -1420,7 +1425,7 @@ class HipBackend:
         self._live(w, scales, biases, ids, op="quantizedEmbedding")
         V = w.shape[0]
         K = w.shape[1] * 8 // opts.bits
-        dt = scales._meta.get("deq_dtype", scales.dtype)
+        dt = (scales._meta or {}).get("deq_dtype", scales.dtype)
         i = self._contiguous(ids if ids.dtype == "i32" else self.cast(ids, "i32"))
         out = self._new(ids.shape + (K,), dt)
         if out.size:
