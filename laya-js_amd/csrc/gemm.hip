@@ -929,6 +929,40 @@ __global__ __launch_bounds__(256) void gemm_simt(int dt, const void* __restrict_
   }
 }
 
+// Small outputs with a long K (M * N <= 16384, K >= 256: a classifier on
+// pooled vectors, the decision head's layers): one wave per output element,
+// lanes striding K with coalesced loads of the X row and the W row(s), then a
+// wave reduction and gemm_simt's epilogue.  The tiled kernel would take one
+// global round trip per 16 columns of K on a handful of blocks.
+__global__ __launch_bounds__(256) void gemm_dot(int dt, const void* __restrict__ X, int64_t ldx,
+                                                const void* __restrict__ W, QWs qw, const void* __restrict__ bias,
+                                                const void* __restrict__ R, int64_t ldr, void* __restrict__ Y,
+                                                int64_t ldy, int M, int N, int K, int geglu) {
+  const int lane = threadIdx.x & 63;
+  const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // output m * N + n, one per wave
+  if (o >= (int64_t)M * N) return;                                   // whole waves
+  const int m = (int)(o / N), n = (int)(o - (int64_t)m * N);
+  float a0 = 0.f, a1 = 0.f;
+  for (int k = lane; k < K; k += 64) {
+    const float x = load_f(X, (int64_t)m * ldx + k, dt);
+    a0 = fmaf(x, simt_w(dt, W, qw, n, k, K), a0);
+    if (geglu) a1 = fmaf(x, simt_w(dt, W, qw, (int64_t)n + N, k, K), a1);
+  }
+  a0 = wave_sum(a0);
+  a1 = wave_sum(a1);
+  if (lane != 0) return;
+  float v = a0 + (bias ? load_f(bias, n, dt) : 0.f);
+  v = round_to(v, dt);
+  if (geglu) {
+    const float g = round_to(a1 + (bias ? load_f(bias, N + n, dt) : 0.f), dt);
+    v = gelu_erf(v) * g;
+  }
+  if (R) v = round_to(v, dt) + load_f(R, (int64_t)m * ldr + n, dt);
+  store_f(Y, (int64_t)m * ldy + n, dt, v);
+}
+
+static bool dot_shape(int64_t M, int64_t N, int64_t K) { return M * N <= 16384 && K >= 256; }
+
 // ------------------------------------------------------------------ dispatch
 
 template <int BM, int BN, int WM, int WN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
@@ -1055,8 +1089,13 @@ extern "C" int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintpt
   } else {
     QWs qw{nullptr, nullptr, nullptr, 0, 0, 1, 0, 0};
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
-    gemm_simt<<<grid, 256, 0, st>>>(dt, (const void*)x, ldx, (const void*)w, qw, b, r, ldr, (void*)y, ldy, (int)M,
-                                    (int)N, (int)K, geglu ? 1 : 0);
+    if (dot_shape(M, N, K)) {
+      gemm_dot<<<(unsigned)((M * N + 3) / 4), 256, 0, st>>>(dt, (const void*)x, ldx, (const void*)w, qw, b, r, ldr,
+                                                           (void*)y, ldy, (int)M, (int)N, (int)K, geglu ? 1 : 0);
+    } else {
+      gemm_simt<<<grid, 256, 0, st>>>(dt, (const void*)x, ldx, (const void*)w, qw, b, r, ldr, (void*)y, ldy, (int)M,
+                                      (int)N, (int)K, geglu ? 1 : 0);
+    }
   }
   check_launch("hb_linear");
   HB_API_END
@@ -1102,8 +1141,13 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
   } else {
     QWs q{(const uint8_t*)qw, (const void*)scales, (const void*)zeros, HB_F16, G, group, bits, mode};
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
-    gemm_simt<<<grid, 256, 0, st>>>(dt, (const void*)x, ldx, nullptr, q, b, r, ldr, (void*)y, ldy, (int)M, (int)N,
-                                    (int)K, geglu ? 1 : 0);
+    if (dot_shape(M, N, K)) {
+      gemm_dot<<<(unsigned)((M * N + 3) / 4), 256, 0, st>>>(dt, (const void*)x, ldx, nullptr, q, b, r, ldr, (void*)y,
+                                                           ldy, (int)M, (int)N, (int)K, geglu ? 1 : 0);
+    } else {
+      gemm_simt<<<grid, 256, 0, st>>>(dt, (const void*)x, ldx, nullptr, q, b, r, ldr, (void*)y, ldy, (int)M, (int)N,
+                                      (int)K, geglu ? 1 : 0);
+    }
   }
   check_launch("hb_qlinear");
   HB_API_END
