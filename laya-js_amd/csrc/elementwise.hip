@@ -530,12 +530,112 @@ int hb_reduce(uintptr_t ctx, int op, int dt_x, uintptr_t x, int64_t outer, int64
   HB_API_END
 }
 
+// Softmax and sort of contiguous rows of 16..1024 values (the decision
+// head's rows of marker scores): one block of 256 threads per row.  Softmax:
+// block max and sum reductions in a fixed order.  Sort: the row goes through
+// y in y's dtype first (the value scan_kernel sorts), then a bitonic sort in
+// LDS on (value, original index) with NaN after every number and ties kept in
+// their original order -- the result of scan_kernel's stable insertion
+// sort, -0 / +0 order included.
+constexpr int kRowMax = 1024;
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();  // red is free (a previous reduction has been read)
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+__global__ __launch_bounds__(256) void row_block_kernel(int op, int dt_x, const void* __restrict__ x, int64_t n,
+                                                        int dt_y, void* __restrict__ y) {
+  __shared__ float kf[kRowMax];
+  __shared__ int32_t ki[kRowMax];
+  __shared__ int32_t ix[kRowMax];
+  __shared__ float red[4];
+  const int64_t base = (int64_t)blockIdx.x * n;
+  const int tid = threadIdx.x;
+  if (op == HB_SCAN_SOFTMAX) {
+    float m = -INFINITY;
+    for (int64_t j = tid; j < n; j += 256) m = fmaxf(m, load_f(x, base + j, dt_x));
+    m = block_reduce(m, true, red);
+    float sum = 0.f;
+    for (int64_t j = tid; j < n; j += 256) sum += expf(load_f(x, base + j, dt_x) - m);
+    const float inv = 1.0f / block_reduce(sum, false, red);
+    for (int64_t j = tid; j < n; j += 256) store_f(y, base + j, dt_y, expf(load_f(x, base + j, dt_x) - m) * inv);
+    return;
+  }
+  const bool in_int = is_int_dt(dt_x), out_int = is_int_dt(dt_y);
+  int P = 1;
+  while (P < n) P <<= 1;
+  for (int j = tid; j < P; j += 256) {
+    if (j < n) {
+      // through y's dtype, element by element in the same thread (no
+      // cross-thread dependence on the global write)
+      if (in_int) store_i(y, base + j, dt_y, load_i(x, base + j, dt_x));
+      else store_f(y, base + j, dt_y, load_f(x, base + j, dt_x));
+      if (out_int) ki[j] = load_i(y, base + j, dt_y);
+      else kf[j] = load_f(y, base + j, dt_y);
+    }
+    ix[j] = j;  // j >= n: padding, after everything
+  }
+  __syncthreads();
+  auto greater = [&](int a, int b) -> bool {  // slot a sorts after slot b
+    const int ia = ix[a], ib = ix[b];
+    const bool pa = ia >= n, pb = ib >= n;
+    if (pa != pb) return pa;
+    if (!pa) {
+      if (out_int) {
+        if (ki[a] != ki[b]) return ki[a] > ki[b];
+      } else {
+        const float fa = kf[a], fb = kf[b];
+        const bool na = fa != fa, nb = fb != fb;
+        if (na != nb) return na;
+        if (!na && fa != fb) return fa > fb;
+      }
+    }
+    return ia > ib;
+  };
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int jj = k >> 1; jj > 0; jj >>= 1) {
+      for (int i = tid; i < P; i += 256) {
+        const int l = i ^ jj;
+        if (l > i && greater(i, l) == ((i & k) == 0)) {
+          const int32_t t = ix[i];
+          ix[i] = ix[l];
+          ix[l] = t;
+          if (out_int) {
+            const int32_t u = ki[i];
+            ki[i] = ki[l];
+            ki[l] = u;
+          } else {
+            const float u = kf[i];
+            kf[i] = kf[l];
+            kf[l] = u;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int64_t j = tid; j < n; j += 256) {
+    if (out_int) store_i(y, base + j, dt_y, ki[j]);
+    else store_f(y, base + j, dt_y, kf[j]);
+  }
+}
+
 int hb_scan(uintptr_t ctx, int op, int dt_x, uintptr_t x, int64_t outer, int64_t n, int64_t inner, int dt_y,
             uintptr_t y) {
   HB_API_BEGIN
   HB_REQUIRE(op >= HB_SCAN_SOFTMAX && op <= HB_SCAN_SORT, "hb_scan: bad op");
   int64_t total = outer * inner;
   if (total == 0 || n == 0) return 0;
+  if (op != HB_SCAN_CUMSUM && inner == 1 && n >= 16 && n <= kRowMax && outer <= 0x7fffffff) {
+    row_block_kernel<<<(unsigned)outer, 256, 0, stream_of(ctx)>>>(op, dt_x, (const void*)x, n, dt_y, (void*)y);
+    check_launch("hb_scan");
+    return 0;
+  }
   scan_kernel<<<grid_for(total, 256), 256, 0, stream_of(ctx)>>>(op, dt_x, (const void*)x, outer, n, inner, dt_y,
                                                                  (void*)y);
   check_launch("hb_scan");
