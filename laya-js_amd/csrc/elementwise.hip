@@ -517,6 +517,32 @@ int hb_gather(uintptr_t ctx, int dt, uintptr_t table, int64_t V, int64_t D, uint
   HB_API_END
 }
 
+// Float sum / mean / max / min of contiguous rows of 64 or more values: one
+// block of 256 threads per row, a wave tree and then the four waves in a
+// fixed order.  Max and min keep reduce_kernel's rule: a NaN wins.
+__device__ __forceinline__ float red_comb(int op, float a, float b) {
+  if (op == HB_RED_SUM || op == HB_RED_MEAN) return a + b;
+  if (op == HB_RED_MAX) return (b > a || b != b) ? b : a;
+  return (b < a || b != b) ? b : a;
+}
+
+__global__ __launch_bounds__(256) void reduce_row_kernel(int op, int dt_x, const void* __restrict__ x, int64_t n,
+                                                         int dt_y, void* __restrict__ y) {
+  __shared__ float red[4];
+  const int64_t base = (int64_t)blockIdx.x * n;
+  const bool additive = op == HB_RED_SUM || op == HB_RED_MEAN;
+  float acc = additive ? 0.f : load_f(x, base, dt_x);  // max / min: seeded with an element of the row
+  for (int64_t j = threadIdx.x; j < n; j += 256) acc = red_comb(op, acc, load_f(x, base + j, dt_x));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc = red_comb(op, acc, __shfl_xor(acc, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  float v = red_comb(op, red_comb(op, red_comb(op, red[0], red[1]), red[2]), red[3]);
+  if (op == HB_RED_MEAN) v /= (float)n;
+  store_f(y, blockIdx.x, dt_y, v);
+}
+
 int hb_reduce(uintptr_t ctx, int op, int dt_x, uintptr_t x, int64_t outer, int64_t n, int64_t inner, int dt_y,
               uintptr_t y) {
   HB_API_BEGIN
@@ -524,6 +550,12 @@ int hb_reduce(uintptr_t ctx, int op, int dt_x, uintptr_t x, int64_t outer, int64
   HB_REQUIRE(n > 0 || op == HB_RED_SUM || op == HB_RED_MEAN, "hb_reduce: empty axis");
   int64_t total = outer * inner;
   if (total == 0) return 0;
+  const bool fl = !is_int_dt(dt_x) || !is_int_dt(dt_y);  // reduce_kernel's float path
+  if (fl && op <= HB_RED_MEAN && inner == 1 && n >= 64 && outer <= 0x7fffffff) {
+    reduce_row_kernel<<<(unsigned)outer, 256, 0, stream_of(ctx)>>>(op, dt_x, (const void*)x, n, dt_y, (void*)y);
+    check_launch("hb_reduce");
+    return 0;
+  }
   reduce_kernel<<<grid_for(total, 256), 256, 0, stream_of(ctx)>>>(op, dt_x, (const void*)x, outer, n, inner, dt_y,
                                                                    (void*)y);
   check_launch("hb_reduce");

@@ -74,3 +74,27 @@ def test_softmax_rows(b, n):
     want = e / e.sum(-1, keepdims=True)
     assert np.max(np.abs(got - want)) <= 1e-6
     b.dispose(X)
+
+
+@pytest.mark.parametrize("n", [63, 64, 255, 1000])
+@pytest.mark.parametrize("op", ["sum", "mean", "max", "min"])
+def test_reduce_rows(b, op, n):
+    """Float reductions over contiguous rows (`sum(plogp, -1)` in the head):
+    rows of 64 or more values take one block per row.  Sum and mean within
+    1e-5 of f64 (relative to the row's sum of |x|); max and min exact, a NaN
+    in the row winning as in numpy."""
+    rng = np.random.default_rng(300 + n)
+    x = rng.standard_normal((6, n)).astype(np.float32)
+    x[3, n // 3] = np.nan
+    X = b.fromHost(HostTensor("f32", x.shape, x))
+    got = np.asarray(b.read(getattr(b, op)(X, -1)).data, np.float32)
+    want = getattr(np, op)(x.astype(np.float64), axis=-1)
+    if op in ("sum", "mean"):
+        scale = np.abs(x.astype(np.float64)).sum(-1) / (n if op == "mean" else 1)
+        ok = np.isnan(want) == np.isnan(got)
+        assert ok.all()
+        fin = ~np.isnan(want)
+        assert np.all(np.abs(got[fin] - want[fin]) <= 1e-5 * scale[fin])
+    else:
+        np.testing.assert_array_equal(got, want.astype(np.float32))
+    b.dispose(X)
