@@ -186,3 +186,38 @@ def test_qlinear_one_hot_reads_exact_weights(b, bits, mode):
     np.testing.assert_array_equal(got, want.T)
     E = C.quantized_embedding(b, Q, b.fromHost(HostTensor("i32", (N,), np.arange(N, dtype=np.int32))))
     np.testing.assert_array_equal(b.read(E).data.view(np.uint16), want)
+
+
+def test_small_output_linear_epilogues(b):
+    """Small outputs with a long K (M * N <= 16384, K >= 256) run one wave per
+    output (gemm_dot) with the SIMT kernel's epilogue: f32 GeGLU with bias
+    (K = 300, not a multiple of 8), bias plus a fused residual, and an f32
+    linear on q4 weights, all against the oracle."""
+    from laya_hip import compose as C
+    rng = np.random.default_rng(21)
+    M, N, K = 3, 20, 300
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((2 * N, K)) * 0.1).astype(np.float32)
+    bias = rng.standard_normal(2 * N).astype(np.float32)
+    r = rng.standard_normal((M, N)).astype(np.float32)
+    X, Wt, Bt, R = (b.fromHost(to_host(a, "f32")) for a in (x, w, bias, r))
+    got = read32(b, b.add(R, b.geglu(b.linear(X, Wt, Bt))))
+    want = cr.geglu(cr.linear(x, w, bias)) + r
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+    n_fused = b.stats["linear_fused_resid"]
+    R2 = b.fromHost(to_host(rng.standard_normal((M, 2 * N)).astype(np.float32), "f32"))
+    got = read32(b, b.add(R2, b.linear(X, Wt, Bt)))  # the residual in the epilogue
+    assert b.stats["linear_fused_resid"] == n_fused + 1
+    np.testing.assert_allclose(got, cr.linear(x, w, bias) + read32(b, R2), rtol=1e-5, atol=1e-5)
+    b.dispose(R2)
+    M, N, K = 4, 64, 512
+    h, q, sf, zf = _quantized(rng, N, K, 4)
+    Q = C.upload_quantized(b, h, "f32")
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    Xq = b.fromHost(to_host(x, "f32"))
+    got = read32(b, C.quantized_linear(b, Xq, Q))
+    want = cr.quantized_linear(x, q, sf, zf, 64, dtype="f32")
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+    C.dispose_quantized(b, Q)
+    for t in (X, Wt, Bt, R, Xq):
+        b.dispose(t)
