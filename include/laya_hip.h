@@ -148,6 +148,23 @@ int hb_event_record(uintptr_t ctx, uintptr_t ev);
 int hb_event_elapsed(uintptr_t start, uintptr_t end, float* ms);
 int hb_event_destroy(uintptr_t ev);
 
+/* Stream capture.  No counterpart in the reference's Backend: for callers
+ * that run the same op sequence again and again on small batches, where the
+ * host's per-op launches, not the GPU, bound the time.
+ * hb_capture_begin starts recording the context's stream (relaxed mode);
+ * the ops enqueued until hb_capture_end are recorded, not run, and
+ * hb_capture_end instantiates them as an executable graph.  hb_graph_launch
+ * replays it on the stream: the same kernels on the same device addresses,
+ * so the caller keeps the recorded inputs and outputs alive and rewrites
+ * inputs in place between replays.  Blocks freed while recording stay out
+ * of the pool until hb_graph_destroy.  Between begin and end: no
+ * hb_upload / hb_download / hb_sync, and no op whose one-time set-up uploads
+ * (run the sequence once before recording it). */
+int hb_capture_begin(uintptr_t ctx);
+int hb_capture_end(uintptr_t ctx, uintptr_t* exec);
+int hb_graph_launch(uintptr_t ctx, uintptr_t exec);
+int hb_graph_destroy(uintptr_t ctx, uintptr_t exec);
+
 /* ---------------------------------------------------------------- hot path */
 
 /* y[M, N] = x[M, K] . w[N, K]^T with f32 accumulation and the epilogue in

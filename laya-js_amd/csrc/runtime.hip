@@ -45,6 +45,11 @@ struct Context {
   int next_staging = 0;
   // RoPE cos/sin tables [L][D/2] (float2), keyed by (L, D, base)
   std::map<std::tuple<int64_t, int64_t, double>, void*> rope_tables;
+  // stream capture: blocks freed while capturing stay out of the free list
+  // (a replay still writes them) until their graph is destroyed
+  bool capturing = false;
+  std::vector<void*> held;
+  std::map<void*, std::vector<void*>> graph_held;  // hipGraphExec_t -> held blocks
 };
 
 static size_t size_class(size_t bytes) {
@@ -101,6 +106,10 @@ void pool_free(uintptr_t ctx, void* p) {
   Context* c = C(ctx);
   auto it = c->live.find(p);
   if (it == c->live.end()) throw std::runtime_error("hb_free: pointer is not a live block of this context");
+  if (c->capturing) {  // still live for the graph being recorded
+    c->held.push_back(p);
+    return;
+  }
   size_t sc = it->second;
   c->live.erase(it);
   c->live_bytes -= sc;
@@ -211,6 +220,7 @@ int hb_destroy(uintptr_t ctx) {
   Context* c = C(ctx);
   HB_CHECK_HIP(hipSetDevice(c->device));
   HB_CHECK_HIP(hipStreamSynchronize(c->stream));
+  for (auto& kv : c->graph_held) (void)hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(kv.first));
   for (auto& kv : c->free_list)
     for (void* p : kv.second) (void)hipFree(p);
   for (auto& kv : c->live) (void)hipFree(kv.first);
@@ -341,6 +351,64 @@ int hb_event_elapsed(uintptr_t start, uintptr_t end, float* ms) {
 int hb_event_destroy(uintptr_t ev) {
   HB_API_BEGIN
   HB_CHECK_HIP(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+  HB_API_END
+}
+
+// ---- stream capture (no counterpart in the reference: a recorded forward
+// replayed without per-op host work, for small batches that the host's
+// launches bound)
+
+int hb_capture_begin(uintptr_t ctx) {
+  HB_API_BEGIN
+  Context* c = C(ctx);
+  HB_REQUIRE(!c->capturing, "hb_capture_begin: already capturing");
+  HB_CHECK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed));
+  c->capturing = true;
+  c->held.clear();
+  HB_API_END
+}
+
+int hb_capture_end(uintptr_t ctx, uintptr_t* exec) {
+  HB_API_BEGIN
+  Context* c = C(ctx);
+  HB_REQUIRE(c->capturing, "hb_capture_end: not capturing");
+  HB_REQUIRE(exec, "hb_capture_end: null output");
+  *exec = 0;
+  c->capturing = false;
+  std::vector<void*> held;
+  held.swap(c->held);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(c->stream, &g);
+  hipGraphExec_t x = nullptr;
+  if (e == hipSuccess) e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  if (g) (void)hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    for (void* p : held) pool_free(ctx, p);  // nothing will replay them
+    throw std::runtime_error(std::string("hb_capture_end: ") + hipGetErrorString(e));
+  }
+  c->graph_held[(void*)x] = std::move(held);
+  *exec = reinterpret_cast<uintptr_t>(x);
+  HB_API_END
+}
+
+int hb_graph_launch(uintptr_t ctx, uintptr_t exec) {
+  HB_API_BEGIN
+  Context* c = C(ctx);
+  HB_REQUIRE(c->graph_held.count((void*)exec), "hb_graph_launch: not a graph of this context");
+  HB_CHECK_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), c->stream));
+  HB_API_END
+}
+
+int hb_graph_destroy(uintptr_t ctx, uintptr_t exec) {
+  HB_API_BEGIN
+  Context* c = C(ctx);
+  auto it = c->graph_held.find((void*)exec);
+  HB_REQUIRE(it != c->graph_held.end(), "hb_graph_destroy: not a graph of this context");
+  HB_CHECK_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec)));
+  std::vector<void*> held;
+  held.swap(it->second);
+  c->graph_held.erase(it);
+  for (void* p : held) pool_free(ctx, p);  // reused only by work enqueued after the last replay
   HB_API_END
 }
 

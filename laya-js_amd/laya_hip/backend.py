@@ -364,6 +364,39 @@ class _PendingSdpa:
         return st
 
 
+# ------------------------------------------------------------------ recorded graphs
+
+class HipGraph:
+    """An op sequence recorded by HipBackend.capture.  run() replays it on
+    the backend's stream and returns the output tensor (the same one each
+    time, rewritten by the replay; it belongs to the caller, who disposes it
+    after destroy())."""
+
+    def __init__(self, be: "HipBackend", exec_: int, out: HipTensor, held: list):
+        self.be, self.exec, self.out, self.held = be, exec_, out, held
+        self._st = out._st.retain() if out._st is not None else None  # the graph writes it
+
+    def run(self) -> HipTensor:
+        if not self.exec:
+            raise RuntimeError("HipGraph: used after destroy()")
+        self.be._call("graph", "hb_graph_launch", self.be.ctx, self.exec)
+        return self.out
+
+    def destroy(self) -> None:
+        if not self.exec:
+            return
+        be = self.be
+        if not be._destroyed:
+            be._call("graph", "hb_graph_destroy", be.ctx, self.exec)
+            for ptr, nbytes in self.held:  # reused only by work enqueued after the last replay
+                be._recycle(ptr, nbytes)
+        self.held = []
+        self.exec = 0
+        if self._st is not None:
+            self._st.release()
+            self._st = None
+
+
 # ------------------------------------------------------------------ backend
 
 class HipBackend:
@@ -382,6 +415,7 @@ class HipBackend:
         self._prof_only = self._LAUNCHES
         self._event_pool: list[int] = []
         self._blocks: dict[int, list[int]] = {}
+        self._capture_held: Optional[list] = None  # blocks disposed while a capture records
         self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "sdpa": 0,
                       "sdpa_fused_rope": 0, "copies": 0, "panel_unpacks": 0}
 
@@ -470,8 +504,12 @@ class HipBackend:
         return _Storage(self, p.value, nbytes)
 
     def _recycle(self, ptr: int, nbytes: int):
-        if not self._destroyed:
-            self._blocks.setdefault(self._size_class(nbytes), []).append(ptr)
+        if self._destroyed:
+            return
+        if self._capture_held is not None:  # a replay of the graph being recorded still writes it
+            self._capture_held.append((ptr, nbytes))
+            return
+        self._blocks.setdefault(self._size_class(nbytes), []).append(ptr)
 
     def _return_blocks(self):
         for ptrs in self._blocks.values():
@@ -760,6 +798,48 @@ class HipBackend:
             self._blocks.clear()  # the library frees every block with the context
             self._call("destroy", "hb_destroy", self.ctx)
             self._destroyed = True
+
+    def capture(self, fn: Callable[[], Any], warmup: bool = True) -> "HipGraph":
+        """Records the launches of `fn()` (an op sequence on this backend)
+        into a HIP graph; HipGraph.run() replays them and returns the same
+        output tensor, rewritten.  No counterpart in the reference's
+        Backend: for small batches, where the host's per-op launches bound
+        the time.  The graph keeps using the device addresses it recorded:
+        the tensors `fn` reads must stay alive (rewrite inputs in place
+        between replays), and blocks disposed while recording stay out of
+        the pool until HipGraph.destroy().  `warmup` runs `fn` once eagerly
+        first, so one-time set-up that uploads (RoPE tables, mask tile
+        classes) happens outside the recording."""
+        if self._capture_held is not None:
+            raise RuntimeError("capture: already recording")
+        if warmup:
+            self.dispose(self._ready(fn()))
+        self.flush()
+        held: list = []
+        self._capture_held = held
+        self._call("capture", "hb_capture_begin", self.ctx)
+        e = F.U(0)
+        try:
+            out = fn()
+            self._ready(out)  # the result's pending launches belong to the recording
+        except BaseException:
+            self._capture_held = None
+            try:
+                self._call("capture", "hb_capture_end", self.ctx, F.C.byref(e))
+                self._call("capture", "hb_graph_destroy", self.ctx, e.value)
+            except Exception:
+                pass
+            for ptr, nbytes in held:
+                self._recycle(ptr, nbytes)
+            raise
+        self._capture_held = None
+        try:
+            self._call("capture", "hb_capture_end", self.ctx, F.C.byref(e))
+        except BaseException:
+            for ptr, nbytes in held:
+                self._recycle(ptr, nbytes)
+            raise
+        return HipGraph(self, e.value, out, held)
 
     def pool_stats(self) -> dict:
         self._return_blocks()  # blocks waiting for reuse count as cached, not live

@@ -52,6 +52,10 @@ SYMBOLS: dict[str, tuple] = {
     "hb_event_record": (I, [U, U]),
     "hb_event_elapsed": (I, [U, U, C.POINTER(F)]),
     "hb_event_destroy": (I, [U]),
+    "hb_capture_begin": (I, [U]),
+    "hb_capture_end": (I, [U, PU64]),
+    "hb_graph_launch": (I, [U, U]),
+    "hb_graph_destroy": (I, [U, U]),
     "hb_linear": (I, [U, I, U, I64, U, U, U, I64, U, I64, I64, I64, I64, C.c_uint]),
     "hb_qlinear": (I, [U, I, U, I64, U, U, U, U, U, I64, U, I64, I64, I64, I64, I, I, I, C.c_uint]),
     "hb_qgather": (I, [U, U, U, U, I64, I64, I, I, I, U, I64, I, U]),

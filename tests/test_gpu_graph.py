@@ -1,0 +1,87 @@
+"""A recorded encoder forward (HipBackend.capture, hb_capture_* /
+hb_graph_*): replays give the eager forward's bits.  Each replay is followed
+by eager work on the same backend (an eager encode, which reuses blocks of
+the pool) and a read that synchronizes; every replay is checked.  New token
+ids written in place into the recorded input give the eager result for those
+ids.  Destroying the graph returns its blocks: the pool's live block count
+comes back to where it was before the recording."""
+import numpy as np
+import pytest
+
+from laya_hip import ffi as F
+from laya_hip.host import HostTensor
+from laya_hip.modernbert import loadModernBert, parseModernBertConfig
+
+pytestmark = pytest.mark.gpu
+
+CFG = {"vocab_size": 1000, "hidden_size": 256, "intermediate_size": 384, "num_hidden_layers": 4,
+       "num_attention_heads": 4, "local_attention": 64}
+
+
+@pytest.fixture(scope="module")
+def b():
+    from laya_hip.backend import HipBackend
+    be = HipBackend(0)
+    yield be
+    be.destroy()
+
+
+def _weights(rng):
+    H, I, V = CFG["hidden_size"], CFG["intermediate_size"], CFG["vocab_size"]
+    n = lambda *s: (rng.standard_normal(s) * 0.02).astype(np.float16)  # noqa: E731
+    W = {"embeddings.tok_embeddings.weight": n(V, H), "embeddings.norm.weight": np.ones(H, np.float16),
+         "final_norm.weight": np.ones(H, np.float16)}
+    for i in range(CFG["num_hidden_layers"]):
+        p = f"layers.{i}."
+        if i:
+            W[p + "attn_norm.weight"] = np.ones(H, np.float16)
+        W[p + "attn.Wqkv.weight"] = n(3 * H, H)
+        W[p + "attn.Wo.weight"] = n(H, H)
+        W[p + "mlp_norm.weight"] = np.ones(H, np.float16)
+        W[p + "mlp.Wi.weight"] = n(2 * I, H)
+        W[p + "mlp.Wo.weight"] = n(H, I)
+    return W
+
+
+def _bits(b, t):
+    return np.asarray(b.read(t).data).view(np.uint16).copy()
+
+
+@pytest.mark.parametrize("B,T", [(1, 128), (2, 96)])
+def test_recorded_encoder_replays(b, B, T):
+    rng = np.random.default_rng(B * 100 + T)
+    W = _weights(rng)
+    enc = loadModernBert(b, parseModernBertConfig(CFG),
+                         lambda nm: HostTensor("f16", W[nm[8:]].shape, W[nm[8:]])
+                         if nm.startswith("encoder.") and nm[8:] in W else None, dtype="f16")
+    ids = rng.integers(0, CFG["vocab_size"], (B, T)).astype(np.int32)
+    valid = np.ones((B, T), np.uint8)
+    valid[-1, T - 17:] = 0  # a padded tail in the last sequence
+    inp = enc.uploadInputs(ids, valid, B, T)
+
+    def eager():
+        y = enc.encode(inp)
+        out = _bits(b, y)
+        b.dispose(y)
+        return out
+
+    want = eager()
+    blocks0 = b.pool_stats()["live_blocks"]
+    g = b.capture(lambda: enc.encode(inp))
+    for _ in range(3):
+        got = _bits(b, g.run())
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(eager(), want)  # eager work between replays
+    # new ids, written in place into the recorded input
+    ids2 = rng.integers(0, CFG["vocab_size"], (B, T)).astype(np.int32)
+    b._call("upload", "hb_upload", b.ctx, b._ptr(inp["ids"]), ids2.ctypes.data, ids2.nbytes)
+    got2 = _bits(b, g.run())
+    want2 = eager()
+    np.testing.assert_array_equal(got2, want2)
+    assert not np.array_equal(want2, want)
+    out = g.out
+    g.destroy()
+    b.dispose(out)  # the recorded output belongs to the caller
+    assert b.pool_stats()["live_blocks"] == blocks0
+    enc.disposeInputs(inp)
+    enc.dispose()
