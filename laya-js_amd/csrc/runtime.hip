@@ -82,6 +82,9 @@ void* pool_alloc(uintptr_t ctx, size_t bytes) {
     c->cached_bytes -= sc;
   } else {
     hipError_t e = hipMalloc(&p, sc);
+    if (e != hipSuccess && c->capturing)  // the retry below would synchronize the recording stream
+      throw std::runtime_error("hb_alloc: out of device memory for " + std::to_string(bytes) +
+                               " bytes while recording a graph");
     if (e != hipSuccess) {
       // release the cache once and retry before failing
       HB_CHECK_HIP(hipStreamSynchronize(c->stream));
@@ -140,6 +143,8 @@ static Staging& staging_for(Context* c, size_t bytes) {
 static constexpr size_t kStageChunk = 64u << 20;
 
 static void upload_raw(Context* c, void* dst, const void* src, size_t bytes) {
+  if (c->capturing)  // a recorded copy would re-read the staging buffer at every replay
+    throw std::runtime_error("upload while recording a graph (run the sequence once before recording it)");
   size_t done = 0;
   while (done < bytes) {
     size_t n = bytes - done < kStageChunk ? bytes - done : kStageChunk;
@@ -297,6 +302,7 @@ int hb_upload(uintptr_t ctx, uintptr_t dst, const void* src, size_t bytes) {
 int hb_download(uintptr_t ctx, void* dst, uintptr_t src, size_t bytes) {
   HB_API_BEGIN
   Context* c = C(ctx);
+  HB_REQUIRE(!c->capturing, "hb_download: the stream is recording a graph");
   HB_REQUIRE(bytes == 0 || (dst && src), "hb_download: null pointer");
   size_t done = 0;
   while (done < bytes) {
@@ -320,6 +326,7 @@ int hb_copy(uintptr_t ctx, uintptr_t dst, uintptr_t src, size_t bytes) {
 
 int hb_sync(uintptr_t ctx) {
   HB_API_BEGIN
+  HB_REQUIRE(!C(ctx)->capturing, "hb_sync: the stream is recording a graph");
   HB_CHECK_HIP(hipStreamSynchronize(C(ctx)->stream));
   HB_API_END
 }

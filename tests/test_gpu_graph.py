@@ -85,3 +85,23 @@ def test_recorded_encoder_replays(b, B, T):
     assert b.pool_stats()["live_blocks"] == blocks0
     enc.disposeInputs(inp)
     enc.dispose()
+
+
+def test_recording_refuses_synchronizing_calls(b):
+    """A read inside a recording is refused with a clear error (the host-side
+    check runs before the stream is touched); the recording is dropped and
+    the backend keeps working eagerly."""
+    x = b.fromHost(HostTensor("f32", (4, 64), np.ones((4, 64), np.float32)))
+
+    def bad():
+        y = b.scale(x, 2.0)
+        b.read(y)
+        return y
+
+    with pytest.raises(F.HipError, match="recording a graph"):
+        b.capture(bad, warmup=False)
+    assert b._capture_held is None
+    y = b.scale(x, 3.0)
+    np.testing.assert_array_equal(np.asarray(b.read(y).data).reshape(4, 64), np.full((4, 64), 3.0, np.float32))
+    for t in (x, y):
+        b.dispose(t)
