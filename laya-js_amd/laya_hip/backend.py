@@ -377,7 +377,7 @@ class HipGraph:
         self._st = out._st.retain() if out._st is not None else None  # the graph writes it
 
     def run(self) -> HipTensor:
-        if not self.exec:
+        if not self.exec or self.be._destroyed:
             raise RuntimeError("HipGraph: used after destroy()")
         self.be._call("graph", "hb_graph_launch", self.be.ctx, self.exec)
         return self.out
