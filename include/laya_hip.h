@@ -214,7 +214,7 @@ int hb_layernorm(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt_w, ui
  * LayerNorm whose consumer is a large-M linear layer (the encoder's
  * attn_norm -> Wqkv and mlp_norm -> Wi, modernbert/src/index.ts:347-354).
  * Same arithmetic as hb_layernorm's 16-bit path, bit for bit; needs dt_x
- * f16 or bf16, D % 256 == 0, D <= 2048, ldx % 4 == 0, x 8-byte aligned and
+ * f16 or bf16, D % 256 == 0, D <= 2048, ldx % 8 == 0, x and y 16-byte aligned and
  * the parameters aligned for 4-wide loads (8 bytes; 16 for f32).  Padding
  * rows of the last block are written as zeros. */
 int hb_layernorm_panel(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt_w, uintptr_t w, uintptr_t b,

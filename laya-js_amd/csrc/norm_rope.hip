@@ -28,113 +28,125 @@ __device__ __forceinline__ void load4_param(const void* p, int c, float (&v)[4])
   }
 }
 
-// One row of the 16-bit path: raw[g] holds columns (g * 64 + lane) * 4 + 0..3
-// of the row; out[g] gets the normalised values at the same columns.  Both
-// 16-bit kernels below call this, so their outputs agree bit for bit.
+// One row of the 16-bit path, held by a half-wave (32 lanes, `hl` = lane
+// % 32): raw[g] holds columns (g * 32 + hl) * 8 + 0..7 of the row (one
+// 16-byte load each); out[g] gets the normalised values at the same
+// columns.  The sums reduce over the half-wave only, so the two halves of a
+// wave normalise two rows side by side.  Both 16-bit kernels below call
+// this, so their outputs agree bit for bit.
+__device__ __forceinline__ float half_wave_sum(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 template <int G, bool BF, int PK>
-__device__ __forceinline__ void ln_row(const uint2v (&raw)[G], int lane, const void* __restrict__ w,
-                                       const void* __restrict__ b, int D, float eps, uint2v (&out)[G]) {
-  float v[G][4];
+__device__ __forceinline__ void ln_row(const uint4v (&raw)[G], int hl, const void* __restrict__ w,
+                                       const void* __restrict__ b, int D, float eps, uint4v (&out)[G]) {
+  float v[G][8];
   float s = 0.0f;
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    const uint16_t h[4] = {(uint16_t)(raw[g].x & 0xffff), (uint16_t)(raw[g].x >> 16), (uint16_t)(raw[g].y & 0xffff),
-                           (uint16_t)(raw[g].y >> 16)};
+    const uint32_t wd[4] = {raw[g].x, raw[g].y, raw[g].z, raw[g].w};
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      v[g][e] = BF ? bf16_to_f32(h[e]) : f16_bits_to_f32(h[e]);
+    for (int e = 0; e < 8; e++) {
+      const uint16_t h = (uint16_t)(wd[e >> 1] >> (16 * (e & 1)));
+      v[g][e] = BF ? bf16_to_f32(h) : f16_bits_to_f32(h);
       s += v[g][e];
     }
   }
-  const float mean = wave_sum(s) / (float)D;
+  const float mean = half_wave_sum(s) / (float)D;
   float q = 0.0f;
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
+    for (int e = 0; e < 8; e++) {
       const float d = v[g][e] - mean;
       q += d * d;
     }
-  const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)D + eps);
+  const float rstd = 1.0f / sqrtf(half_wave_sum(q) / (float)D + eps);
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    const int c = (g * 64 + lane) * 4;
-    float wv[4] = {1.f, 1.f, 1.f, 1.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
+    const int c = (g * 32 + hl) * 8;
+    float wv[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f}, bv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if constexpr (PK != 0) {
-      if (w) load4_param<PK>(w, c, wv);
-      if (b) load4_param<PK>(b, c, bv);
-    }
-    uint16_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      float t = (v[g][e] - mean) * rstd;
-      if constexpr (PK != 0) {
-        if (w) t = pin_f32(t * wv[e]);
-        if (b) t += bv[e];
+      if (w) {
+        load4_param<PK>(w, c, *(float(*)[4])(wv));
+        load4_param<PK>(w, c + 4, *(float(*)[4])(wv + 4));
       }
-      o[e] = BF ? f32_to_bf16(t) : f32_to_f16_bits(t);
+      if (b) {
+        load4_param<PK>(b, c, *(float(*)[4])(bv));
+        load4_param<PK>(b, c + 4, *(float(*)[4])(bv + 4));
+      }
     }
-    out[g] = uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      uint16_t r2[2];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        float t = (v[g][e + k] - mean) * rstd;
+        if constexpr (PK != 0) {
+          if (w) t = pin_f32(t * wv[e + k]);
+          if (b) t += bv[e + k];
+        }
+        r2[k] = BF ? f32_to_bf16(t) : f32_to_f16_bits(t);
+      }
+      o[e >> 1] = (uint32_t)r2[0] | ((uint32_t)r2[1] << 16);
+    }
+    out[g] = uint4v{o[0], o[1], o[2], o[3]};
   }
 }
 
+// Row-major output: 8 rows per block of 256 threads, one per half-wave.
 template <int G, bool BF, int PK>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                             const void* __restrict__ w, const void* __restrict__ b,
                                                             uint16_t* __restrict__ y, int64_t rows, int D, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int hl = threadIdx.x & 31;
+  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (row >= rows) return;  // a whole half-wave: its sums never read the other half
   const uint16_t* xr = x + row * ldx;
-  uint2v raw[G], out[G];
+  uint4v raw[G], out[G];
 #pragma unroll
-  for (int g = 0; g < G; g++) raw[g] = *(const uint2v*)(xr + (g * 64 + lane) * 4);
-  ln_row<G, BF, PK>(raw, lane, w, b, D, eps, out);
+  for (int g = 0; g < G; g++) raw[g] = *(const uint4v*)(xr + (g * 32 + hl) * 8);
+  ln_row<G, BF, PK>(raw, hl, w, b, D, eps, out);
   uint16_t* yr = y + row * (int64_t)D;
 #pragma unroll
-  for (int g = 0; g < G; g++) *(uint2v*)(yr + (g * 64 + lane) * 4) = out[g];
+  for (int g = 0; g < G; g++) *(uint4v*)(yr + (g * 32 + hl) * 8) = out[g];
 }
 
-// Panel-order output: a block of 512 threads normalises 8 consecutive rows,
-// one per wave (two per wave in 256-thread blocks measured 6% slower: a
-// wave's normalisations run one after the other).  In panel order those
-// rows' chunks of one (16-column block, half) pair form one 128-byte line, so
-// the block stages its rows in LDS line by line -- chunk of row i in line l at
-// slot (i + l) % 8, which spreads a wave's writes over the banks -- and writes
-// each line whole with 8 consecutive 16-byte stores.  The grid covers the
-// padding rows of the last 32-row block, which are written as zeros.
-constexpr int kLnRpw = 1, kLnNT = 64 * 8 / kLnRpw;  // rows per wave, threads per block (8 rows)
+// Panel-order output: a block of 256 threads normalises 8 consecutive rows,
+// one per half-wave.  In panel order those rows' chunks of one (16-column
+// block, half) pair form one 128-byte line, so the block stages its rows in
+// LDS line by line -- chunk of row i in line l at slot (i + l) % 8, which
+// spreads a half-wave's writes over the banks -- and writes each line whole
+// with 8 consecutive 16-byte stores.  The grid covers the padding rows of the
+// last 32-row block, which are written as zeros.
+constexpr int kLnNT = 256;  // threads per block (8 rows)
 template <int G, bool BF, int PK>
 __global__ __launch_bounds__(kLnNT) void layernorm_panel_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                              const void* __restrict__ w, const void* __restrict__ b,
-                                                              uint16_t* __restrict__ y, int64_t rows, int D,
-                                                              float eps) {
+                                                                const void* __restrict__ w,
+                                                                const void* __restrict__ b, uint16_t* __restrict__ y,
+                                                                int64_t rows, int D, float eps) {
   extern __shared__ __attribute__((aligned(16))) uint16_t tile[];  // [D / 8 lines][8 slots][8]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hl = threadIdx.x & 31, r = threadIdx.x >> 5;
   const int64_t row0 = (int64_t)blockIdx.x * 8;
-  uint2v raw[kLnRpw][G];
+  const int64_t row = row0 + r;
+  const uint16_t* xr = x + (row < rows ? row : rows - 1) * ldx;
+  uint4v raw[G], out[G];
 #pragma unroll
-  for (int i = 0; i < kLnRpw; i++) {
-    const int64_t row = row0 + wave * kLnRpw + i;
-    const uint16_t* xr = x + (row < rows ? row : rows - 1) * ldx;
+  for (int g = 0; g < G; g++) raw[g] = *(const uint4v*)(xr + (g * 32 + hl) * 8);
+  if (row < rows) {
+    ln_row<G, BF, PK>(raw, hl, w, b, D, eps, out);
+  } else {
 #pragma unroll
-    for (int g = 0; g < G; g++) raw[i][g] = *(const uint2v*)(xr + (g * 64 + lane) * 4);
+    for (int g = 0; g < G; g++) out[g] = uint4v{0, 0, 0, 0};
   }
 #pragma unroll
-  for (int i = 0; i < kLnRpw; i++) {
-    const int r = wave * kLnRpw + i;
-    uint2v out[G];
-    if (row0 + r < rows) {
-      ln_row<G, BF, PK>(raw[i], lane, w, b, D, eps, out);
-    } else {
-#pragma unroll
-      for (int g = 0; g < G; g++) out[g] = uint2v{0, 0};
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      const int c = (g * 64 + lane) * 4, l = c >> 3;
-      *(uint2v*)(tile + l * 64 + ((r + l) & 7) * 8 + (c & 7)) = out[g];
-    }
+  for (int g = 0; g < G; g++) {
+    const int l = g * 32 + hl;  // the chunk's line: columns 8l .. 8l + 7
+    *(uint4v*)(tile + l * 64 + ((r + l) & 7) * 8) = out[g];
   }
   __syncthreads();
   const int64_t kb = D >> 4;  // 16-column blocks per row
@@ -202,8 +214,8 @@ static int ln_param_kind(int dt_w, uintptr_t w, uintptr_t b) {
 // The 16-bit kernels' conditions (besides the output's).
 static bool ln_vec_ok(int dt_x, uintptr_t x, int64_t ldx, int pk, uintptr_t w, uintptr_t b, int64_t D) {
   const int64_t pal = pk == 3 ? 16 : 8;  // parameter alignment the 4-wide loads need
-  return (dt_x == HB_F16 || dt_x == HB_BF16) && D % 256 == 0 && D <= 2048 && ldx % 4 == 0 && x % 8 == 0 && pk >= 0 &&
-         w % pal == 0 && b % pal == 0;
+  return (dt_x == HB_F16 || dt_x == HB_BF16) && D % 256 == 0 && D <= 2048 && ldx % 8 == 0 && x % 16 == 0 &&
+         pk >= 0 && w % pal == 0 && b % pal == 0;
 }
 
 static void launch_ln16(bool panel, hipStream_t st, bool bf, int pk, const uint16_t* x, int64_t ldx, uintptr_t w,
@@ -226,7 +238,7 @@ static void launch_ln16(bool panel, hipStream_t st, bool bf, int pk, const uint1
                                                                   eps);
     } else {
       auto kern = bf ? layernorm_vec_kernel<GG, true, PP> : layernorm_vec_kernel<GG, false, PP>;
-      kern<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(x, ldx, (const void*)w, (const void*)b, y, rows, D, eps);
+      kern<<<(unsigned)((rows + 7) / 8), 256, 0, st>>>(x, ldx, (const void*)w, (const void*)b, y, rows, D, eps);
     }
   };
   auto by_g = [&](auto pc) {
@@ -262,7 +274,7 @@ int hb_layernorm(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt_w, ui
   if (rows == 0) return 0;
   hipStream_t st = stream_of(ctx);
   const int pk = ln_param_kind(dt_w, w, b);
-  if (dt_y == dt_x && ln_vec_ok(dt_x, x, ldx, pk, w, b, D) && y % 8 == 0) {
+  if (dt_y == dt_x && ln_vec_ok(dt_x, x, ldx, pk, w, b, D) && y % 16 == 0) {
     launch_ln16(false, st, dt_x == HB_BF16, pk, (const uint16_t*)x, ldx, w, b, (uint16_t*)y, rows, (int)D, eps);
   } else {
     layernorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(dt_x, (const void*)x, ldx, dt_w, (const void*)w,
@@ -278,7 +290,7 @@ int hb_layernorm_panel(uintptr_t ctx, int dt_x, uintptr_t x, int64_t ldx, int dt
   HB_REQUIRE(D > 0 && ldx >= D, "hb_layernorm_panel: bad row width");
   const int pk = ln_param_kind(dt_w, w, b);
   HB_REQUIRE(ln_vec_ok(dt_x, x, ldx, pk, w, b, D) && y % 16 == 0,
-             "hb_layernorm_panel: needs f16/bf16, D % 256 == 0, D <= 2048, ldx % 4 == 0 and aligned operands");
+             "hb_layernorm_panel: needs f16/bf16, D % 256 == 0, D <= 2048, ldx % 8 == 0 and 16-byte aligned operands");
   if (rows == 0) return 0;
   launch_ln16(true, stream_of(ctx), dt_x == HB_BF16, pk, (const uint16_t*)x, ldx, w, b, (uint16_t*)y, rows, (int)D,
               eps);

@@ -189,7 +189,7 @@ class _PendingNorm:
         # hb_layernorm_panel's conditions
         pal = 16 if wdt == "f32" else 8
         self.panel_ok = (x.dtype in ("f16", "bf16") and dt == x.dtype and D % 256 == 0 and D <= 2048 and
-                         ld % 4 == 0 and xp % 8 == 0 and wdt in (None, "f16", "bf16", "f32") and wp % pal == 0 and
+                         ld % 8 == 0 and xp % 16 == 0 and wdt in (None, "f16", "bf16", "f32") and wp % pal == 0 and
                          bp % pal == 0)
 
     def release(self):
