@@ -115,3 +115,18 @@ def test_parse_config_matches_fixture():
         parseModernBertConfig({**cfgj, "layer_types": ["full_attention"]})
     with pytest.raises(ValueError, match="RoPE"):
         parseModernBertConfig({**cfgj, "rope_parameters": {"full_attention": {"rope_type": "yarn"}}})
+
+
+def test_block_size_classes_match_the_library_rule():
+    """HipBackend keeps disposed blocks by the library pool's size class
+    (runtime.hip, size_class): 256-byte steps up to 64 KiB, then steps of a
+    sixteenth of the next power of two."""
+    sc = HipBackend._size_class
+    assert [sc(n) for n in (0, 1, 255, 256, 257, 65536)] == [256, 256, 256, 256, 512, 65536]
+    assert sc(65537) == 65536 + 8192  # next power 131072, step 8192
+    assert sc(100_000) == 106496  # 13 * 8192
+    assert sc(1 << 20) == 1 << 20
+    assert sc((1 << 20) + 1) == (1 << 20) + (1 << 17)  # next power 2 MiB, step 128 KiB
+    for n in (1, 300, 4096, 70_000, 3_000_000, 123_456_789):
+        c = sc(n)
+        assert c >= n and sc(c) == c  # a class is its own class
