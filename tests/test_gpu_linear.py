@@ -163,6 +163,31 @@ def test_qlinear_config2(b, name, M, bits):
     b.dispose(X)
 
 
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("M", [512, 4160])
+def test_qlinear_bf16(b, M, bits):
+    """Quantized weights with bf16 activations: the dequantized weight is
+    rounded once to bf16 (quant.ts:189-243, dequantRows then the compute
+    dtype) on both kernels -- M = 512 (the small-M kernel, weight stages
+    loaded two ahead) and M = 4160 (the large-M kernel, a partial row tile) --
+    against the oracle's dequantize-then-linear in bf16, max-rel <= 1e-2."""
+    from laya_hip import compose as C
+    N, K = SHAPES["Wqkv"]
+    rng = np.random.default_rng(7 * M + bits)
+    h, q, sf, zf = _quantized(rng, N, K, bits)
+    x = rounded(rng.standard_normal((M, K)), "bf16")
+    X = b.fromHost(to_host(x, "bf16"))
+    Q = C.upload_quantized(b, h, "bf16")
+    assert Q.native
+    got = read32(b, C.quantized_linear(b, X, Q))
+    rows = _rows(M, rng)
+    ref = cr.quantized_linear(x[rows], q, sf, zf, 64, dtype="bf16")
+    err = max_rel(got[rows], ref)
+    assert err <= 1e-2, f"bf16 M={M} q{bits}: max-rel {err:.2e}"
+    C.dispose_quantized(b, Q)
+    b.dispose(X)
+
+
 @pytest.mark.parametrize("bits,mode", [(8, "symmetric"), (4, "affine"), (8, "affine"), (4, "symmetric")])
 def test_qlinear_one_hot_reads_exact_weights(b, bits, mode):
     """x = identity rows: y[k, n] = dequant(W)[n, k] must equal fl16(q*s + z)
