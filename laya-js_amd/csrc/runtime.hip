@@ -53,7 +53,7 @@ struct Context {
 };
 
 static size_t size_class(size_t bytes) {
-  // 256-byte granularity up to 64 KiB, then steps of 1/8 of the power of two
+  // 256-byte granularity up to 64 KiB, then steps of 1/16 of the next power of two
   if (bytes == 0) bytes = 1;
   if (bytes <= 65536) return (bytes + 255) & ~(size_t)255;
   size_t p = 1;
