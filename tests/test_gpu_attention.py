@@ -86,6 +86,40 @@ def test_sdpa_encoder_layout_config3(b, kind, dtype):
         assert err <= tol, f"(b={bb}, h={hh}, len={lens[bb]}): max-rel {err:.2e}"
 
 
+@pytest.mark.parametrize("kind", ["full_attention", "sliding_attention"])
+def test_sdpa_at_the_maximum_sequence_length(b, kind):
+    """One sequence of ModernBERT's max_position_embeddings (8192) tokens with
+    a padded tail, through the encoder's call (rope(q), rope(k), strided views
+    of one projection).  Query rows are independent, so the oracle runs on a
+    sample of them: both ends of a 128-query tile, the middle of the
+    sequence, the last valid query and padded queries (which attend to every
+    valid key under the sliding mask)."""
+    print(f"sdpa L=8192 {kind}", flush=True)
+    rng = np.random.default_rng(6)
+    B, L, nh, hd, n_valid = 1, 8192, 12, 64, 7192
+    valid = (np.arange(L)[None, :] < n_valid).astype(np.uint8)
+    full, sliding = attentionMasks(valid, B, L, 128)
+    mask_h = full if kind == "full_attention" else sliding
+    base = 160000.0 if kind == "full_attention" else 10000.0
+    qkv = rounded(rng.standard_normal((B, L, 3 * nh * hd)), "f16")
+    dev = b.fromHost(to_host(qkv, "f16"))
+    mask = b.fromHost(mask_h)
+    q, k, v = _qkv_views(b, dev, B, L, nh, hd)
+    got = read32(b, b.sdpa(b.rope(q, base), b.rope(k, base), v, mask, hd ** -0.5))
+    sel = np.array([0, 1, 127, 128, 4095, 4096, 7000, n_valid - 1, n_valid, L - 1])
+    t = qkv.reshape(B, L, 3, nh, hd).transpose(2, 0, 3, 1, 4)
+    for hh in (0, 11):
+        qs, ks, vs = (np.ascontiguousarray(t[i][:, hh:hh + 1]) for i in range(3))
+        rq = rounded(cr.rope(qs, base), "f16")[:, :, sel]
+        rk = rounded(cr.rope(ks, base), "f16")
+        m = mask_h.data if kind == "full_attention" else mask_h.data[:, :, sel]
+        ref = cr.sdpa(rq, rk, vs, m, hd ** -0.5)
+        err = max_rel(got[:, hh:hh + 1, sel], ref)
+        assert err <= 5e-3, f"(h={hh}): max-rel {err:.2e}"
+    for x in (dev, mask):
+        b.dispose(x)
+
+
 def test_sdpa_fused_rope_is_bit_identical_to_separate_rope(b):
     rng = np.random.default_rng(4)
     B, L, nh, hd = 2, 300, 12, 64
