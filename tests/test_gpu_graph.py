@@ -1,7 +1,9 @@
 """A recorded encoder forward (HipBackend.capture, hb_capture_* /
 hb_graph_*): replays give the eager forward's bits.  Each replay is followed
 by eager work on the same backend (an eager encode, which reuses blocks of
-the pool) and a read that synchronizes; every replay is checked.  New token
+the pool) and a read that synchronizes; every replay is checked.  The shapes
+take both GEMM kernels: the small-M one, and at M = 4096 rows the large-M one
+with panel-order operands from the LayerNorm, attention and GeGLU kernels.  New token
 ids written in place into the recorded input give the eager result for those
 ids.  Destroying the graph returns its blocks: the pool's live block count
 comes back to where it was before the recording."""
@@ -47,7 +49,7 @@ def _bits(b, t):
     return np.asarray(b.read(t).data).view(np.uint16).copy()
 
 
-@pytest.mark.parametrize("B,T", [(1, 128), (2, 96)])
+@pytest.mark.parametrize("B,T", [(1, 128), (2, 96), (8, 512)])  # M = 4096: the large-M GEMM, panel operands
 def test_recorded_encoder_replays(b, B, T):
     rng = np.random.default_rng(B * 100 + T)
     W = _weights(rng)
