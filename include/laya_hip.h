@@ -109,7 +109,10 @@ const char* hb_last_error(void);
 int hb_abi_version(void);
 
 /* Opens device `device` and creates a context with one stream.
- * Replaces createMlxBackend's device/stream setup (backend-mlx/src/index.ts:920). */
+ * Replaces createMlxBackend's device/stream setup (backend-mlx/src/index.ts:920).
+ * It makes `device` current on the calling thread.  A context's later calls
+ * need that device current: calls that would create device memory or events
+ * fail with an error while another device is current. */
 int hb_init(int device, uintptr_t* ctx);
 /* Frees every pooled block and the stream.  Backend.destroy (index.ts:165-166). */
 int hb_destroy(uintptr_t ctx);

@@ -4,6 +4,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
 #include <stdint.h>
+#include <atomic>
 #include <string>
 
 #include "../../include/laya_hip.h"
@@ -25,6 +26,19 @@ void set_error(const std::string& msg);
     if (!(cond)) throw std::runtime_error(std::string(msg));         \
   } while (0)
 void check_launch(const char* what);
+
+// Runs `set` (a kernel attribute setting, which applies to the current
+// device) once per device: bit d of `done` records device d.  Concurrent
+// first calls may both run `set`, which is idempotent.
+template <class Set>
+inline void once_per_device(std::atomic<uint64_t>& done, Set&& set) {
+  int dev = 0;
+  HB_CHECK_HIP(hipGetDevice(&dev));
+  const uint64_t bit = 1ull << (dev & 63);
+  if (done.load(std::memory_order_acquire) & bit) return;
+  set();
+  done.fetch_or(bit, std::memory_order_acq_rel);
+}
 
 struct Context;
 hipStream_t stream_of(uintptr_t ctx);

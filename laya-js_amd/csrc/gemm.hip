@@ -975,11 +975,10 @@ static void launch_mfma(hipStream_t st, const uint16_t* x, int64_t ldx, const ui
   size_t ctile = (size_t)BM * BNO * sizeof(uint16_t);
   size_t lds = stage > ctile ? stage : ctile;
   auto kern = gemm_mfma<BM, BN, WM, WN, BF16, GEGLU, QB, AFF, SF32>;
-  static bool attr = false;
-  if (!attr) {
+  static std::atomic<uint64_t> attr{0};
+  once_per_device(attr, [&] {
     HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attr = true;
-  }
+  });
   kern<<<tiles_m * tiles_n, WM * WN * 64, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n);
 }
 
@@ -998,11 +997,10 @@ static void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x
   constexpr int RG = (BNO / 8 + 7) / 8;
   const size_t lds = ((size_t)2 * BN * 64 + (size_t)RG * 256 * 64) * sizeof(uint16_t);
   auto kern = gemm_mfma_arow<BN, BF16, GEGLU, QB, AFF, SF32, KTAIL>;
-  static bool attr = false;
-  if (!attr) {
+  static std::atomic<uint64_t> attr{0};
+  once_per_device(attr, [&] {
     HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attr = true;
-  }
+  });
   kern<<<grid, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n, tiles, (pan & HB_X_PANEL) ? 1 : 0,
                                (pan & HB_Y_PANEL) ? 1 : 0);
 }

@@ -225,14 +225,13 @@ static void launch_ln16(bool panel, hipStream_t st, bool bf, int pk, const uint1
     constexpr int GG = decltype(gc)::value, PP = decltype(pc)::value;
     if (panel) {
       constexpr size_t lds = (size_t)8 * GG * 256 * sizeof(uint16_t);  // 8 rows
-      static bool attr = false;
-      if (!attr) {
+      static std::atomic<uint64_t> attr{0};
+      once_per_device(attr, [&] {
         HB_CHECK_HIP(hipFuncSetAttribute((const void*)layernorm_panel_kernel<GG, true, PP>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         HB_CHECK_HIP(hipFuncSetAttribute((const void*)layernorm_panel_kernel<GG, false, PP>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-      }
+      });
       auto kern = bf ? layernorm_panel_kernel<GG, true, PP> : layernorm_panel_kernel<GG, false, PP>;
       kern<<<(unsigned)((rows + 31) / 32 * 4), kLnNT, lds, st>>>(x, ldx, (const void*)w, (const void*)b, y, rows, D,
                                                                   eps);

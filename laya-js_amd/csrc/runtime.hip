@@ -71,6 +71,19 @@ hipStream_t stream_of(uintptr_t ctx) { return C(ctx)->stream; }
 int device_of(uintptr_t ctx) { return C(ctx)->device; }
 int cu_count(uintptr_t ctx) { return C(ctx)->cus; }
 
+// Device memory and events belong to the current device, so a context
+// creates them only while its own device is current (hb_init makes it
+// current on the calling thread); otherwise the call fails instead of
+// placing them on another device.
+static void require_current(const Context* c) {
+  int dev = -1;
+  HB_CHECK_HIP(hipGetDevice(&dev));
+  if (dev != c->device)
+    throw std::runtime_error("context of device " + std::to_string(c->device) + " used while device " +
+                             std::to_string(dev) + " is current (call hipSetDevice(" + std::to_string(c->device) +
+                             ") on this thread first)");
+}
+
 void* pool_alloc(uintptr_t ctx, size_t bytes) {
   Context* c = C(ctx);
   size_t sc = size_class(bytes);
@@ -81,6 +94,7 @@ void* pool_alloc(uintptr_t ctx, size_t bytes) {
     it->second.pop_back();
     c->cached_bytes -= sc;
   } else {
+    require_current(c);
     hipError_t e = hipMalloc(&p, sc);
     if (e != hipSuccess && c->capturing)  // the retry below would synchronize the recording stream
       throw std::runtime_error("hb_alloc: out of device memory for " + std::to_string(bytes) +
@@ -135,7 +149,10 @@ static Staging& staging_for(Context* c, size_t bytes) {
     HB_CHECK_HIP(hipHostMalloc(&s.host, cap, hipHostMallocDefault));
     s.cap = cap;
   }
-  if (!s.done) HB_CHECK_HIP(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
+  if (!s.done) {
+    require_current(c);
+    HB_CHECK_HIP(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
+  }
   return s;
 }
 
@@ -181,6 +198,7 @@ const float* rope_table(uintptr_t ctx, int64_t L, int64_t D, double base) {
     }
   }
   void* d = nullptr;
+  require_current(c);
   HB_CHECK_HIP(hipMalloc(&d, tab.size() * sizeof(float) + 16));
   upload_raw(c, d, tab.data(), tab.size() * sizeof(float));
   c->rope_tables[key] = d;
@@ -333,8 +351,8 @@ int hb_sync(uintptr_t ctx) {
 
 int hb_event_create(uintptr_t ctx, uintptr_t* ev) {
   HB_API_BEGIN
-  (void)C(ctx);
   HB_REQUIRE(ev, "hb_event_create: null output");
+  require_current(C(ctx));
   hipEvent_t e;
   HB_CHECK_HIP(hipEventCreate(&e));
   *ev = reinterpret_cast<uintptr_t>(e);
