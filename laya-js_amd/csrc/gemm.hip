@@ -1151,6 +1151,24 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
   HB_API_END
 }
 
+// One dequantized table value: the code times its group's f16 scale (plus the
+// f16 zero when affine).  f16 output: f16 arithmetic (an exact product rounded
+// once, or one fused multiply-add); f32 output: one rounding of the exact value.
+__device__ __forceinline__ float qg_value(int code, uint16_t s_bits, uint16_t z_bits, int aff, bool out_f16) {
+  const float s = f16_bits_to_f32(s_bits);
+  if (out_f16) {
+    f16 sh = (f16)s, qh = (f16)(float)code;
+    f16 w = aff ? __builtin_fmaf16(qh, sh, (f16)f16_bits_to_f32(z_bits)) : (f16)(qh * sh);
+    return (float)w;
+  }
+  return aff ? fmaf((float)code, s, f16_bits_to_f32(z_bits)) : (float)code * s;  // q*s is exact in f32
+}
+
+__device__ __forceinline__ int qg_code(uint32_t u, int bits, int aff) {
+  if (bits == 8) return aff ? (int)u : (int)(int8_t)(uint8_t)u;
+  return aff ? (int)u : (((int)u ^ 8) - 8);
+}
+
 __global__ void qgather_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ scales,
                                const uint16_t* __restrict__ zeros, int64_t V, int64_t K, int bits, int G, int group,
                                int aff, const int32_t* __restrict__ ids, int64_t n, int dt_out,
@@ -1160,25 +1178,63 @@ __global__ void qgather_kernel(const uint8_t* __restrict__ q, const uint16_t* __
     int64_t r = i / K, k = i - r * K;
     int64_t id = ids[r];
     id = id < 0 ? 0 : (id >= V ? V - 1 : id);
-    int code;
+    uint32_t u;
     if (bits == 8) {
-      uint8_t u = q[id * K + k];
-      code = aff ? (int)u : (int)(int8_t)u;
+      u = q[id * K + k];
     } else {
-      uint8_t u = q[id * (K / 2) + k / 2];
-      int v = (k & 1) ? (u >> 4) : (u & 15);
-      code = aff ? v : ((v ^ 8) - 8);
+      const uint8_t b = q[id * (K / 2) + k / 2];
+      u = (k & 1) ? (b >> 4) : (b & 15);
     }
     int64_t gi = id * G + k / group;
-    float s = f16_bits_to_f32(scales[gi]);
-    if (dt_out == HB_F16) {
-      f16 sh = (f16)s, qh = (f16)(float)code;
-      f16 w = aff ? __builtin_fmaf16(qh, sh, (f16)f16_bits_to_f32(zeros[gi])) : (f16)(qh * sh);
-      store_f(out, i, dt_out, (float)w);
+    const float w = qg_value(qg_code(u, bits, aff), scales[gi], aff ? zeros[gi] : (uint16_t)0, aff,
+                             dt_out == HB_F16);
+    store_f(out, i, dt_out, w);
+  }
+}
+
+// K % 8 == 0 and group % 8 == 0: one thread per 8 consecutive values of a
+// row, which share one group.  One 8-byte (q8) or 4-byte (q4) code load, one
+// scale (and zero) load, and 16-byte stores (one for f16, two for f32).  The
+// values are qg_value's, as in qgather_kernel.
+template <int BITS, bool OUT16>
+__global__ __launch_bounds__(256) void qgather8_kernel(const uint8_t* __restrict__ q,
+                                                       const uint16_t* __restrict__ scales,
+                                                       const uint16_t* __restrict__ zeros, int V, int K, int G,
+                                                       int group, int aff, const int32_t* __restrict__ ids,
+                                                       int chunks, void* __restrict__ out) {
+  const int kc = K >> 3;
+  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += gridDim.x * blockDim.x) {
+    const int r = c / kc, k0 = (c - r * kc) << 3;
+    int id = ids[r];
+    id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+    uint32_t w0, w1 = 0;
+    if (BITS == 8) {
+      const uint2v v = *(const uint2v*)(q + (int64_t)id * K + k0);
+      w0 = v.x;
+      w1 = v.y;
     } else {
-      // f32 with one rounding of the exact value (q*s is exact in f32)
-      float w = aff ? fmaf((float)code, s, f16_bits_to_f32(zeros[gi])) : (float)code * s;
-      store_f(out, i, dt_out, w);
+      w0 = *(const uint32_t*)(q + (int64_t)id * (K >> 1) + (k0 >> 1));
+    }
+    const int64_t gi = (int64_t)id * G + k0 / group;
+    const uint16_t sb = scales[gi], zb = aff ? zeros[gi] : (uint16_t)0;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const uint32_t u = BITS == 8 ? (((e < 4 ? w0 : w1) >> (8 * (e & 3))) & 255u) : ((w0 >> (4 * e)) & 15u);
+      v[e] = qg_value(qg_code(u, BITS, aff), sb, zb, aff, OUT16);
+    }
+    const int64_t o = (int64_t)r * K + k0;
+    if (OUT16) {
+      uint4v pk;
+      pk.x = (uint32_t)f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
+      pk.y = (uint32_t)f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
+      pk.z = (uint32_t)f32_to_f16_bits(v[4]) | ((uint32_t)f32_to_f16_bits(v[5]) << 16);
+      pk.w = (uint32_t)f32_to_f16_bits(v[6]) | ((uint32_t)f32_to_f16_bits(v[7]) << 16);
+      *(uint4v*)((uint16_t*)out + o) = pk;
+    } else {
+      float4v* d = (float4v*)((float*)out + o);
+      d[0] = float4v{v[0], v[1], v[2], v[3]};
+      d[1] = float4v{v[4], v[5], v[6], v[7]};
     }
   }
 }
@@ -1192,7 +1248,28 @@ extern "C" int hb_qgather(uintptr_t ctx, uintptr_t qw, uintptr_t scales, uintptr
   int64_t total = n * K;
   if (total == 0) return 0;
   int G = (int)((K + group - 1) / group);
-  qgather_kernel<<<grid_for(total, 256), 256, 0, stream_of(ctx)>>>((const uint8_t*)qw, (const uint16_t*)scales,
+  hipStream_t st = stream_of(ctx);
+  const bool out16 = dt_out == HB_F16;
+  if ((out16 || dt_out == HB_F32) && K % 8 == 0 && group % 8 == 0 && out % 16 == 0 && qw % (bits == 8 ? 8 : 4) == 0 &&
+      ids % 4 == 0 && V < (1ll << 31) && K < (1ll << 30) && total / 8 < (1ll << 30)) {
+    // chunks < 2^30: the grid-stride index stays below 2^31
+    const int chunks = (int)(total / 8);
+    const unsigned grid = grid_for(chunks, 256);
+    const uint8_t* Q = (const uint8_t*)qw;
+    const uint16_t *S = (const uint16_t*)scales, *Z = (const uint16_t*)zeros;
+    const int32_t* I = (const int32_t*)ids;
+    if (bits == 8 && out16)
+      qgather8_kernel<8, true><<<grid, 256, 0, st>>>(Q, S, Z, (int)V, (int)K, G, group, mode, I, chunks, (void*)out);
+    else if (bits == 8)
+      qgather8_kernel<8, false><<<grid, 256, 0, st>>>(Q, S, Z, (int)V, (int)K, G, group, mode, I, chunks, (void*)out);
+    else if (out16)
+      qgather8_kernel<4, true><<<grid, 256, 0, st>>>(Q, S, Z, (int)V, (int)K, G, group, mode, I, chunks, (void*)out);
+    else
+      qgather8_kernel<4, false><<<grid, 256, 0, st>>>(Q, S, Z, (int)V, (int)K, G, group, mode, I, chunks, (void*)out);
+    check_launch("hb_qgather");
+    return 0;
+  }
+  qgather_kernel<<<grid_for(total, 256), 256, 0, st>>>((const uint8_t*)qw, (const uint16_t*)scales,
                                                                    (const uint16_t*)zeros, V, K, bits, G, group, mode,
                                                                    (const int32_t*)ids, n, dt_out, (void*)out);
   check_launch("hb_qgather");
