@@ -637,7 +637,10 @@ static void sdpa_impl(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uin
   const float2* tq = rope_q > 0 ? (const float2*)rope_table(ctx, Lq, D, rope_q) : nullptr;
   const float2* tk = rope_k > 0 ? (const float2*)rope_table(ctx, Lk, D, rope_k) : nullptr;
   S4 Qs = s4(qs), Ks = s4(ks), Vs = s4(vs), Ms = s4(ms), Os = s4(os);
-  bool fast = (dt == HB_F16 || dt == HB_BF16) && D == 64 && qs[3] == 1 && ks[3] == 1 && vs[3] == 1 && os[3] == 1 &&
+  // No keys (Lk == 0): every row is fully masked; the generic kernel gives
+  // such rows 0/0 = NaN, as it and the MFMA kernel do for a row whose keys
+  // are all masked, and needs no mask summary.
+  bool fast = Lk > 0 && (dt == HB_F16 || dt == HB_BF16) && D == 64 && qs[3] == 1 && ks[3] == 1 && vs[3] == 1 && os[3] == 1 &&
               q % 16 == 0 && k % 16 == 0 && v % 16 == 0 && o % 8 == 0 && qs[2] % 8 == 0 && ks[2] % 8 == 0 &&
               vs[2] % 8 == 0 && qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 &&
               vs[0] % 8 == 0 && vs[1] % 8 == 0 && os[0] % 4 == 0 && os[1] % 4 == 0 && os[2] % 4 == 0 &&

@@ -101,7 +101,9 @@ class _Storage:
         self.ptr = ptr
         self.nbytes = nbytes
         self.refs = 1
-        self.cache: Optional[dict] = None  # device summaries derived from this storage, created on first use
+        # device summaries derived from this storage's contents, created on
+        # first use: key -> [device pointer, fresh]
+        self.cache: Optional[dict] = None
 
     def retain(self):
         self.refs += 1
@@ -111,8 +113,8 @@ class _Storage:
         self.refs -= 1
         if self.refs == 0 and self.ptr:
             if self.cache:
-                for p in self.cache.values():
-                    self.owner._free(p)
+                for ent in self.cache.values():
+                    self.owner._free(ent[0])
             self.cache = None
             self.owner._recycle(self.ptr, self.nbytes)
             self.ptr = 0
@@ -416,6 +418,7 @@ class HipBackend:
         self._event_pool: list[int] = []
         self._blocks: dict[int, list[int]] = {}
         self._capture_held: Optional[list] = None  # blocks disposed while a capture records
+        self._capture_summaries: Optional[set] = None  # summaries already enqueued into the recording
         self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "sdpa": 0,
                       "sdpa_fused_rope": 0, "copies": 0, "panel_unpacks": 0}
 
@@ -788,10 +791,15 @@ class HipBackend:
                 self.dispose(t)
         return result
 
-    def flush(self, *ts: HipTensor) -> None:
+    def flush(self, *ts: HipTensor, wait: bool = True) -> None:
+        """Forces pending lazy work of `ts` to execute (index.ts:163-164):
+        their launches are enqueued now; with `wait` (the default) the call
+        also waits for the stream."""
         for t in ts:
+            self._live(t, op="flush")
             self._ready(t)
-        self._call("flush", "hb_sync", self.ctx)
+        if wait:
+            self._call("flush", "hb_sync", self.ctx)
 
     def destroy(self) -> None:
         if not self._destroyed:
@@ -806,10 +814,12 @@ class HipBackend:
         Backend: for small batches, where the host's per-op launches bound
         the time.  The graph keeps using the device addresses it recorded:
         the tensors `fn` reads must stay alive (rewrite inputs in place
-        between replays), and blocks disposed while recording stay out of
-        the pool until HipGraph.destroy().  `warmup` runs `fn` once eagerly
-        first, so one-time set-up that uploads (RoPE tables, mask tile
-        classes) happens outside the recording."""
+        between replays with `write`), and blocks disposed while recording
+        stay out of the pool until HipGraph.destroy().  Device summaries of
+        the inputs (mask tile classes) are recomputed by every replay.
+        `warmup` runs `fn` once eagerly first, so one-time set-up that
+        allocates or uploads (RoPE tables, summary buffers) happens outside
+        the recording."""
         if self._capture_held is not None:
             raise RuntimeError("capture: already recording")
         if warmup:
@@ -817,6 +827,7 @@ class HipBackend:
         self.flush()
         held: list = []
         self._capture_held = held
+        self._capture_summaries = set()
         self._call("capture", "hb_capture_begin", self.ctx)
         e = F.U(0)
         try:
@@ -824,6 +835,7 @@ class HipBackend:
             self._ready(out)  # the result's pending launches belong to the recording
         except BaseException:
             self._capture_held = None
+            self._capture_summaries = None
             try:
                 self._call("capture", "hb_capture_end", self.ctx, F.C.byref(e))
                 self._call("capture", "hb_graph_destroy", self.ctx, e.value)
@@ -833,6 +845,7 @@ class HipBackend:
                 self._recycle(ptr, nbytes)
             raise
         self._capture_held = None
+        self._capture_summaries = None
         try:
             self._call("capture", "hb_capture_end", self.ctx, F.C.byref(e))
         except BaseException:
@@ -1394,7 +1407,7 @@ class HipBackend:
             refs.append(mc._st.retain())
         info = self._mask_info(mc, ms, B, Lq, Lk) if mc is not None else 0
         # hb_sdpa_panel's conditions (its MFMA path), for a large-M consumer
-        panel_ok = (dt in ("f16", "bf16") and D == 64 and B * Lq >= PANEL_MIN_M and (H * D) % 64 == 0
+        panel_ok = (dt in ("f16", "bf16") and D == 64 and Lk > 0 and B * Lq >= PANEL_MIN_M and (H * D) % 64 == 0
                     and all(p % 16 == 0 for p in (qp, kp, vp)) and all(st_[3] == 1 for st_ in (qs, ks, vs))
                     and all(st_[i] % 8 == 0 for st_ in (qs, ks, vs) for i in range(3))
                     and (ms is None or ms[1] == 0) and (Lk + 63) // 64 <= 1024)
@@ -1407,22 +1420,56 @@ class HipBackend:
 
     def _mask_info(self, mc: HipTensor, ms, B: int, Lq: int, Lk: int) -> int:
         """Device summary of a bool mask (per-tile: no / all / some keys
-        visible), built once per mask view and cached on its storage, so the
-        14 sliding-window layers of an encode share one pass over the mask."""
+        visible), cached on the mask's storage so the 14 sliding-window
+        layers of an encode share one pass over the mask.  It is rebuilt when
+        stale (the mask was rewritten in place by `write`) and, while a graph
+        records, enqueued once into the recording, so every replay
+        summarises the mask as it is at that replay."""
         if ms[1] != 0 or not (B and Lq and Lk):
             return 0
         key = ("sdpa_tiles", mc._off, tuple(ms), B, Lq, Lk)
         if mc._st.cache is None:
             mc._st.cache = {}
         cache = mc._st.cache
-        if key not in cache:
+        ent = cache.get(key)
+        if ent is None:
             n = F.C.c_size_t(0)
             self._call("sdpa", "hb_sdpa_mask_info_bytes", B, Lq, Lk, F.C.byref(n))
             p = F.U(0)
             self._call("sdpa", "hb_alloc", self.ctx, max(1, n.value), F.C.byref(p))
-            self._call("sdpa", "hb_sdpa_mask_info", self.ctx, self._ptr(mc), F.i64s(ms), B, Lq, Lk, p.value)
-            cache[key] = p.value
-        return cache[key]
+            ent = cache[key] = [p.value, False]
+        rec = self._capture_summaries
+        if not ent[1] or (rec is not None and (id(mc._st), key) not in rec):
+            self._call("sdpa", "hb_sdpa_mask_info", self.ctx, self._ptr(mc), F.i64s(ms), B, Lq, Lk, ent[0])
+            ent[1] = True
+            if rec is not None:
+                rec.add((id(mc._st), key))
+        return ent[0]
+
+    def write(self, t: HipTensor, h: HostTensor) -> None:
+        """Overwrites a contiguous tensor's values in place with host data of
+        the same dtype and shape (copied at call time).  No counterpart in the
+        reference's Backend, whose tensors are immutable: it rewrites the
+        inputs of a recorded graph between replays (HipBackend.capture).
+        Device summaries derived from the old contents (attention-mask tile
+        classes) are marked stale and rebuilt on their next use."""
+        self._live(t, op="write")
+        if self._capture_held is not None:
+            raise RuntimeError("write: a graph is recording (rewrite inputs between replays)")
+        if t._lazy is not None or not self._is_contig(t):
+            raise ValueError("write: the tensor must be a materialised, contiguous tensor")
+        dtype = WIDEN.get(h.dtype, h.dtype)
+        if dtype != t.dtype or tuple(int(d) for d in h.shape) != t.shape:
+            raise ValueError(f"write: {h.dtype}[{','.join(map(str, h.shape))}] into "
+                             f"{t.dtype}[{','.join(map(str, t.shape))}]")
+        data = np.asarray(h.data)
+        if dtype == "bool":
+            data = (data != 0).astype(np.uint8)
+        data = np.ascontiguousarray(data, dtype=NP_DTYPE[dtype])
+        if data.nbytes:
+            self._call("write", "hb_upload", self.ctx, self._ptr(t), data.ctypes.data, data.nbytes)
+        for ent in (t._st.cache or {}).values():
+            ent[1] = False
 
     # ---------------------------------------------------------------- optional fused ops
     def geglu(self, x: HipTensor) -> HipTensor:

@@ -12,7 +12,8 @@ the mathematics fixes (the reference's fixtures hold no empty shapes):
 - meanPool over a sequence of length 0 is 0, as compose.ts:96-105 divides by
   max(count, 1);
 - max over an empty axis has no value. It is refused with an error before
-  any launch.
+  any launch;
+- attention over no keys is NaN, like a fully masked query row.
 """
 import numpy as np
 import pytest
@@ -110,3 +111,23 @@ def test_meanpool_of_empty_sequences(b, dtype):
     assert _read(b, b.meanPool(_t(b, dtype, (0, 5, 64)), _t(b, "bool", (0, 5)))).shape == (0, 64)
     for t in (x, mask):
         b.dispose(t)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("masked", [False, True])
+def test_sdpa_without_keys(b, dtype, masked):
+    """Attention over Lk = 0 keys: a softmax over an empty set, 0 / 0, is NaN
+    in every output, as for a query row whose keys are all masked (the
+    oracle's cr_sdpa and both kernels give those rows NaN).  A masked call
+    builds no mask summary and launches nothing invalid.  The query and
+    value shapes are those of the encoder's MFMA path (D = 64)."""
+    q = _t(b, dtype, (2, 3, 40, 64), np.ones(2 * 3 * 40 * 64))
+    k = _t(b, dtype, (2, 3, 0, 64))
+    v = _t(b, dtype, (2, 3, 0, 64))
+    m = _t(b, "bool", (2, 1, 40, 0)) if masked else None
+    o = b.sdpa(q, k, v, m, 0.125)
+    got = _read(b, o).astype(np.float32)
+    assert got.shape == (2, 3, 40, 64) and np.all(np.isnan(got))
+    for t in (q, k, v, m, o):
+        if t is not None:
+            b.dispose(t)

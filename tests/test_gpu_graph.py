@@ -4,15 +4,16 @@ by eager work on the same backend (an eager encode, which reuses blocks of
 the pool) and a read that synchronizes; every replay is checked.  The shapes
 take both GEMM kernels: the small-M one, and at M = 4096 rows the large-M one
 with panel-order operands from the LayerNorm, attention and GeGLU kernels.  New token
-ids written in place into the recorded input give the eager result for those
-ids.  Destroying the graph returns its blocks: the pool's live block count
+ids, and then a new padding pattern in the attention masks, written in place
+into the recorded inputs (HipBackend.write) give the eager result for those
+inputs: every replay re-summarises the masks it reads.  Destroying the graph returns its blocks: the pool's live block count
 comes back to where it was before the recording."""
 import numpy as np
 import pytest
 
 from laya_hip import ffi as F
 from laya_hip.host import HostTensor
-from laya_hip.modernbert import loadModernBert, parseModernBertConfig
+from laya_hip.modernbert import attentionMasks, loadModernBert, parseModernBertConfig
 
 pytestmark = pytest.mark.gpu
 
@@ -76,11 +77,32 @@ def test_recorded_encoder_replays(b, B, T):
         np.testing.assert_array_equal(eager(), want)  # eager work between replays
     # new ids, written in place into the recorded input
     ids2 = rng.integers(0, CFG["vocab_size"], (B, T)).astype(np.int32)
-    b._call("upload", "hb_upload", b.ctx, b._ptr(inp["ids"]), ids2.ctypes.data, ids2.nbytes)
+    b.write(inp["ids"], HostTensor("i32", (B, T), ids2))
     got2 = _bits(b, g.run())
     want2 = eager()
     np.testing.assert_array_equal(got2, want2)
     assert not np.array_equal(want2, want)
+    # a new padding pattern, written in place into the recorded masks: the
+    # replay summarises the new masks (tiles that were hidden are now seen
+    # and the other way round), as does the eager forward after the write
+    valid3 = np.ones((B, T), np.uint8)
+    valid3[0, T // 2 + 3:] = 0
+    if B > 1:
+        valid3[-1, :] = 1
+    full3, sliding3 = attentionMasks(valid3, B, T, CFG["local_attention"])
+    b.write(inp["masks"]["full_attention"], full3)
+    b.write(inp["masks"]["sliding_attention"], sliding3)
+    b.write(inp["mask"], HostTensor("bool", (B, T), valid3))
+    got3 = _bits(b, g.run())
+    want3 = eager()
+    np.testing.assert_array_equal(got3, want3)
+    fresh = enc.uploadInputs(ids2, valid3, B, T)
+    y = enc.encode(fresh)
+    np.testing.assert_array_equal(_bits(b, y), want3)
+    b.dispose(y)
+    enc.disposeInputs(fresh)
+    assert not np.array_equal(want3, want2)
+    np.testing.assert_array_equal(_bits(b, g.run()), want3)  # replays again after eager work
     out = g.out
     g.destroy()
     b.dispose(out)  # the recorded output belongs to the caller
