@@ -31,7 +31,19 @@
  *   masks         ops.json sdpa masks (window 16), as
  *                 modernbert/test/modernbert.test.ts:52-63 does
  *   encoder       tiny activations.json, every stage at 1e-5
+ *   f16 / bf16    every binary16 pattern decoded as numpy does and rounded
+ *                 back to itself; every bfloat16 pattern unchanged, halfway
+ *                 points to even, one ulp either side to the nearer value,
+ *                 overflow to inf; torch's bfloat16 RNE on random values
+ *   f16 storage   encoder_forward(dtype="f16"): layer 0 equals the pinned
+ *                 ops composed with an f16 rounding after each, bit for
+ *                 bit; every stage f16-valued and within 2e-2 of the tiny
+ *                 activations
+ *   decision head (cpu_ref.py) tiny activations.json type_emb_added,
+ *                 head.layers.0/1, logits and act at 1e-5; masked logits
+ *                 exactly -1e4
  */
+#include <immintrin.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -113,30 +125,67 @@ int cr_num_threads(void) {
 
 /* ------------------------------------------------------------------ linear */
 
-/* y[M,N] = x[M,K] . w[N,K]^T (+ b[N]); f64 accumulation, one f32 rounding.
- * Backend.linear, tensor-backend/src/index.ts:211-215. */
+/* Sum of the four lanes. */
+static inline double hsum4(__m256d v) {
+  __m128d lo = _mm256_castpd256_pd128(v), hi = _mm256_extractf128_pd(v, 1);
+  lo = _mm_add_pd(lo, hi);
+  return _mm_cvtsd_f64(_mm_add_sd(lo, _mm_unpackhi_pd(lo, lo)));
+}
+
+/* Dot products of up to 4 rows of a with up to 4 rows of b (f64, length K):
+ * out[r][c] = sum_k a[r][k] b[c][k], accumulated in four f64 lanes over k
+ * (k mod 4), then the lanes and the k tail in order.  Rows past ra / cb
+ * alias row 0 and are not stored. */
+static void dot4x4(const double* const* a, int ra, const double* const* b, int cb, int64_t K, double out[4][4]) {
+  __m256d acc[4][4];
+  for (int r = 0; r < 4; r++)
+    for (int c = 0; c < 4; c++) acc[r][c] = _mm256_setzero_pd();
+  int64_t k = 0;
+  for (; k + 4 <= K; k += 4) {
+    __m256d av[4], bv[4];
+    for (int r = 0; r < 4; r++) av[r] = _mm256_loadu_pd(a[r] + k);
+    for (int c = 0; c < 4; c++) bv[c] = _mm256_loadu_pd(b[c] + k);
+    for (int r = 0; r < 4; r++)
+      for (int c = 0; c < 4; c++) acc[r][c] = _mm256_fmadd_pd(av[r], bv[c], acc[r][c]);
+  }
+  for (int r = 0; r < ra; r++)
+    for (int c = 0; c < cb; c++) {
+      double v = hsum4(acc[r][c]);
+      for (int64_t t = k; t < K; t++) v += a[r][t] * b[c][t];
+      out[r][c] = v;
+    }
+}
+
+/* y[M,N] = x[M,K] . w[N,K]^T (+ b[N]); f64 accumulation (every f32 product
+ * is exact in f64), one f32 rounding.  Backend.linear,
+ * tensor-backend/src/index.ts:211-215. */
 void cr_linear(const float* x, const float* w, const float* b, float* y, int64_t M, int64_t N, int64_t K) {
-  const int64_t RB = 4; /* rows of x per task: each w row is reused 4 times */
+  double* wd = (double*)malloc(sizeof(double) * (size_t)(N * K + 1));
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < N * K; i++) wd[i] = (double)w[i];
+  const int64_t RB = 4;
 #pragma omp parallel for schedule(dynamic, 1)
   for (int64_t r0 = 0; r0 < M; r0 += RB) {
-    int64_t r1 = r0 + RB < M ? r0 + RB : M;
-    double* xd = (double*)malloc(sizeof(double) * (size_t)(RB * K));
-    for (int64_t r = r0; r < r1; r++)
-      for (int64_t k = 0; k < K; k++) xd[(r - r0) * K + k] = (double)x[r * K + k];
-    for (int64_t n = 0; n < N; n++) {
-      const float* wn = w + n * K;
-      double acc[4] = {0, 0, 0, 0};
-      for (int64_t k = 0; k < K; k++) {
-        double wv = (double)wn[k];
-        for (int64_t r = 0; r < r1 - r0; r++) acc[r] += xd[r * K + k] * wv;
-      }
-      for (int64_t r = r0; r < r1; r++) {
-        double v = acc[r - r0] + (b ? (double)b[n] : 0.0);
-        y[r * N + n] = (float)v;
-      }
+    int ra = (int)(r0 + RB < M ? RB : M - r0);
+    double* xd = (double*)malloc(sizeof(double) * (size_t)(RB * K + 1));
+    const double* xr[4];
+    for (int r = 0; r < 4; r++) {
+      xr[r] = xd + (r < ra ? r : 0) * K;
+      if (r < ra)
+        for (int64_t k = 0; k < K; k++) xd[r * K + k] = (double)x[(r0 + r) * K + k];
+    }
+    for (int64_t n0 = 0; n0 < N; n0 += 4) {
+      int cb = (int)(n0 + 4 < N ? 4 : N - n0);
+      const double* wr[4];
+      for (int c = 0; c < 4; c++) wr[c] = wd + (n0 + (c < cb ? c : 0)) * K;
+      double out[4][4];
+      dot4x4(xr, ra, wr, cb, K, out);
+      for (int r = 0; r < ra; r++)
+        for (int c = 0; c < cb; c++) y[(r0 + r) * N + n0 + c] = (float)(out[r][c] + (b ? (double)b[n0 + c] : 0.0));
     }
     free(xd);
   }
+  free(wd);
 }
 
 /* ------------------------------------------------------------------ norms */
@@ -214,33 +263,60 @@ void cr_rope(const float* x, float* y, int64_t BH, int64_t L, int64_t D, double 
  * Backend.sdpa, tensor-backend/src/index.ts:230-237. */
 void cr_sdpa(const float* q, const float* k, const float* v, const uint8_t* mask, const int64_t* ms, float* o,
              int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, double scale) {
+  const int64_t nkv = B * H * Lk * D;
+  double* kd = (double*)malloc(sizeof(double) * (size_t)(nkv + 1));
+  double* vd = (double*)malloc(sizeof(double) * (size_t)(nkv + 1));
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < nkv; t++) {
+    kd[t] = (double)k[t];
+    vd[t] = (double)v[t];
+  }
 #pragma omp parallel for schedule(static) collapse(2)
   for (int64_t bh = 0; bh < B * H; bh++) {
     for (int64_t i = 0; i < Lq; i++) {
       int64_t bb = bh / H, hh = bh % H;
       const float* qi = q + (bh * Lq + i) * D;
-      double* p = (double*)malloc(sizeof(double) * (size_t)Lk);
-      double mx = -INFINITY;
+      double* p = (double*)malloc(sizeof(double) * (size_t)(Lk + 2 * D + 8));
+      int64_t* vis = (int64_t*)malloc(sizeof(int64_t) * (size_t)(Lk + 1));
+      double* qd = p + Lk;   /* q row in f64 */
+      double* acc = qd + D;  /* output row accumulator */
+      for (int64_t d = 0; d < D; d++) qd[d] = (double)qi[d];
+      int64_t nv = 0;
       for (int64_t j = 0; j < Lk; j++) {
-        int vis = 1;
-        if (mask) vis = mask[bb * ms[0] + hh * ms[1] + i * ms[2] + j * ms[3]] != 0;
-        if (!vis) { p[j] = -INFINITY; continue; }
-        const float* kj = k + (bh * Lk + j) * D;
-        double s = 0;
-        for (int64_t d = 0; d < D; d++) s += (double)qi[d] * (double)kj[d];
-        p[j] = s * scale;
-        if (p[j] > mx) mx = p[j];
+        p[j] = -INFINITY;
+        if (!mask || mask[bb * ms[0] + hh * ms[1] + i * ms[2] + j * ms[3]]) vis[nv++] = j;
+      }
+      const double* qa[4] = {qd, qd, qd, qd};
+      double mx = -INFINITY;
+      for (int64_t t = 0; t < nv; t += 4) {  /* four visible keys at a time */
+        int cb = (int)(t + 4 < nv ? 4 : nv - t);
+        const double* ka[4];
+        for (int c = 0; c < 4; c++) ka[c] = kd + (bh * Lk + vis[t + (c < cb ? c : 0)]) * D;
+        double s[4][4];
+        dot4x4(qa, 1, ka, cb, D, s);
+        for (int c = 0; c < cb; c++) {
+          double sc = s[0][c] * scale;
+          p[vis[t + c]] = sc;
+          if (sc > mx) mx = sc;
+        }
       }
       double sum = 0;
       for (int64_t j = 0; j < Lk; j++) { p[j] = p[j] == -INFINITY ? 0.0 : exp(p[j] - mx); sum += p[j]; }
-      for (int64_t d = 0; d < D; d++) {
-        double acc = 0;
-        for (int64_t j = 0; j < Lk; j++) if (p[j] != 0.0) acc += p[j] * (double)v[(bh * Lk + j) * D + d];
-        o[(bh * Lq + i) * D + d] = (float)(acc / sum);
+      /* sum_j p_j v_j, in key order for every d */
+      for (int64_t d = 0; d < D; d++) acc[d] = 0.0;
+      for (int64_t j = 0; j < Lk; j++) {
+        if (p[j] == 0.0) continue;
+        const double pj = p[j];
+        const double* vj = vd + (bh * Lk + j) * D;
+        for (int64_t d = 0; d < D; d++) acc[d] += pj * vj[d];
       }
+      for (int64_t d = 0; d < D; d++) o[(bh * Lq + i) * D + d] = (float)(acc[d] / sum);
+      free(vis);
       free(p);
     }
   }
+  free(kd);
+  free(vd);
 }
 
 /* ------------------------------------------------------------------ gelu */

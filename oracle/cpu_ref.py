@@ -75,7 +75,16 @@ def round_f16(x) -> np.ndarray:
     return y
 
 
+def f16_bits_to_f32(bits) -> np.ndarray:
+    """IEEE binary16 bit patterns decoded exactly to f32."""
+    h = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().cr_f16_bits_to_f32(_p(h), _p(out), I64(h.size))
+    return out
+
+
 def round_bf16(x) -> np.ndarray:
+    """Values rounded through bfloat16 storage (RNE, NaN kept), as f32."""
     y = _f32(x).copy()
     lib().cr_round_bf16(_p(y), I64(y.size))
     return y
@@ -338,3 +347,85 @@ def encoder_forward(cfg: EncoderConfig, W: dict, ids: np.ndarray, valid: np.ndar
     if stages is not None:
         stages["final_norm"] = y
     return y
+
+
+# ---------------------------------------------------------------- decision head
+
+HEAD_EPS = 1e-5
+
+
+def head_layer(W: dict, j: int, x: np.ndarray, mask: np.ndarray, heads: int) -> np.ndarray:
+    """PyTorch pre-norm TransformerEncoderLayer with a ReLU FFN, op for op as
+    laya/src/model.ts:124-138 (names as in laya-mlx checkpoints)."""
+    B, L, D = x.shape
+    hd = D // heads
+    p = f"head.layers.{j}."
+    h = layer_norm(x, W[p + "norm1.weight"], W[p + "norm1.bias"], HEAD_EPS)
+    qkv = linear(h, W[p + "self_attn.in_proj.weight"], W[p + "self_attn.in_proj.bias"])
+    qkv = qkv.reshape(B, L, 3, heads, hd).transpose(2, 0, 3, 1, 4)
+    q, k, v = (np.ascontiguousarray(t) for t in qkv)
+    att = sdpa(q, k, v, mask, hd ** -0.5)
+    att = np.ascontiguousarray(att.transpose(0, 2, 1, 3)).reshape(B, L, D)
+    x1 = x + linear(att, W[p + "self_attn.out_proj.weight"], W[p + "self_attn.out_proj.bias"])
+    f = linear(np.maximum(linear(layer_norm(x1, W[p + "norm2.weight"], W[p + "norm2.bias"], HEAD_EPS),
+                                 W[p + "linear1.weight"], W[p + "linear1.bias"]), np.float32(0)),
+               W[p + "linear2.weight"], W[p + "linear2.bias"])
+    return x1 + f
+
+
+def softmax_rows(x) -> np.ndarray:
+    """Softmax over the last axis in f64, stored f32."""
+    z = np.asarray(x, np.float64)
+    e = np.exp(z - z.max(-1, keepdims=True))
+    return (e / e.sum(-1, keepdims=True)).astype(np.float32)
+
+
+def decision_forward(cfg: EncoderConfig, W: dict, head_layers: int, ids: np.ndarray, valid: np.ndarray,
+                     qtype: np.ndarray, marker_pos: np.ndarray, marker_mask: np.ndarray,
+                     stages: dict | None = None, enc_out: np.ndarray | None = None):
+    """laya's DecisionModel.forwardCore (laya/src/model.ts:178-236) in f32
+    storage: the encoder (``W`` names carry the "encoder." prefix), the type
+    embedding, ``head_layers`` head layers, the marker scorer and the action
+    head.  Returns (logits [B, M] f32 with masked slots -1e4, act [B, nAct]).
+    ``enc_out`` skips the encoder with its precomputed final-norm output."""
+    B, L = ids.shape
+    M = marker_pos.shape[1]
+    D = cfg.hidden
+    if enc_out is None:
+        encW = {k[len("encoder."):]: v for k, v in W.items() if k.startswith("encoder.")}
+        enc_stages = {} if stages is not None else None
+        enc_out = encoder_forward(cfg, encW, ids, valid, stages=enc_stages)
+        if stages is not None:
+            for k, v in enc_stages.items():
+                stages["embeddings" if k == "embeddings" else f"encoder.{k}"] = v
+    h = enc_out + embedding(W["type_emb.weight"], np.asarray(qtype, np.int32))[:, None, :]
+    if stages is not None:
+        stages["type_emb_added"] = h
+    head_mask = (np.asarray(valid).reshape(B, 1, 1, L) != 0).astype(np.uint8)
+    heads = max(1, D // 64)
+    for j in range(head_layers):
+        h = head_layer(W, j, h, head_mask, heads)
+        if stages is not None:
+            stages[f"head.layers.{j}"] = h
+    pos = np.maximum(np.asarray(marker_pos, np.int64), 0)
+    markers = np.ascontiguousarray(h[np.arange(B)[:, None], pos])
+    s1 = gelu(linear(layer_norm(markers, W["scorer.layers.0.weight"], W["scorer.layers.0.bias"], HEAD_EPS),
+                     W["scorer.layers.1.weight"], W["scorer.layers.1.bias"]))
+    scored = linear(s1, W["scorer.layers.3.weight"], W["scorer.layers.3.bias"]).reshape(B, M)
+    mm = np.asarray(marker_mask).reshape(B, M) != 0
+    logits = np.where(mm, scored, np.float32(-1e4)).astype(np.float32)
+    p = softmax_rows(logits)
+    plogp = p * np.log(np.maximum(p, np.float32(1e-9)).astype(np.float64)).astype(np.float32)
+    k = np.maximum(mm.sum(1), 2).astype(np.float32)
+    entropy = (plogp.astype(np.float64).sum(-1).astype(np.float32) * np.float32(-1)) / \
+        np.log(k.astype(np.float64)).astype(np.float32)
+    top = np.sort(p, -1)[:, M - 2:]
+    top2, top1 = top[:, 0:1], top[:, 1:2]
+    features = np.concatenate([top1, top1 - top2, entropy.reshape(B, 1), k.reshape(B, 1) / np.float32(255)], -1)
+    pooled = np.concatenate([h[:, 0, :], features], -1).astype(np.float32)
+    act = linear(gelu(linear(pooled, W["act_head.layers.0.weight"], W["act_head.layers.0.bias"])),
+                 W["act_head.layers.2.weight"], W["act_head.layers.2.bias"])
+    if stages is not None:
+        stages["logits"] = logits
+        stages["act"] = act
+    return logits, act
