@@ -2,9 +2,9 @@
 
 - `HipBackend` / `createHipBackend`: the `Backend` contract on
   libhipbackend.so (hand-written HIP kernels, one stream).
-- `compose`, `host`, `modernbert`: host-side mirrors of the reference's
-  compose helpers, host types and ModernBERT encoder, so callers run
-  unchanged on this backend.
+- `compose`, `host`, `modernbert`, `model`: host-side mirrors of the
+  reference's compose helpers, host types, ModernBERT encoder and laya
+  decision model, so callers run unchanged on this backend.
 
 Importing the package does not touch the GPU; creating a backend loads the
 library and fails loudly when it is missing.
