@@ -1,10 +1,12 @@
 """Benchmark: ModernBERT-base encode tokens/s at B=32, T=512 on one MI355X.
 
 One step = one full encoder forward (embeddings + 22 layers + final norm)
-over a batch of 32 sequences of 512 tokens (lengths uniform in [64, 512],
+over a new batch of 32 sequences of 512 tokens (lengths uniform in [64, 512],
 right-padded), through HipBackend, the laya-js `Backend`
-contract on libhipbackend.so, driven by the unchanged encoder code.  Inputs
-(token ids, masks) are resident on the GPU before the timed region.  Weights
+contract on libhipbackend.so, driven by the unchanged encoder code.  Every
+step encodes a batch of its own (token ids and masks, all resident on the GPU
+before the timed region), so each step also builds its masks' tile summaries,
+and each step launches its whole output, the final LayerNorm included.  Weights
 are random-init fp16 ~N(0, 0.02) with LayerNorm gamma = 1; ids uniform in
 [0, 50368).
 
@@ -90,8 +92,12 @@ def _is_dominant(key: str) -> bool:
 
 
 def _key_flops(key: str) -> float:
+    """2*M*N*K of one linear launch.  The key's N is the launch's output
+    width; a GeGLU launch computes twice that many columns (value and gate)
+    before its epilogue halves them."""
     f = dict(kv.split("=") for kv in key[key.index("[") + 1:key.index("]")].split(",") if "=" in kv)
-    return 2.0 * int(f["M"]) * int(f["N"]) * int(f["K"])
+    n = int(f["N"]) * (2 if "geglu" in key else 1)
+    return 2.0 * int(f["M"]) * n * int(f["K"])
 
 
 def _profiled_traffic():
@@ -107,6 +113,18 @@ def _profiled_traffic():
     return None
 
 
+def make_batches(n: int, B: int, T: int, seed: int) -> list:
+    """n synthetic config-3 batches: ids uniform in [0, 50368), lengths
+    uniform in [64, T], right-padded."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        lens = rng.integers(64, T + 1, B)
+        ids = rng.integers(0, BASE["vocab_size"], (B, T)).astype(np.int32)
+        out.append((ids, (np.arange(T)[None, :] < lens[:, None]).astype(np.uint8)))
+    return out
+
+
 def run_encode(args) -> dict:
     from laya_hip.backend import HipBackend
     from laya_hip.host import HostTensor
@@ -115,10 +133,6 @@ def run_encode(args) -> dict:
     B, T = 32, 512
     cfg = parseModernBertConfig(BASE)
     W = make_weights(BASE)
-    rng = np.random.default_rng(1)
-    lens = rng.integers(64, T + 1, B)
-    ids = rng.integers(0, BASE["vocab_size"], (B, T)).astype(np.int32)
-    valid = (np.arange(T)[None, :] < lens[:, None]).astype(np.uint8)
 
     be = HipBackend(0)
     info = be.device_info()
@@ -126,16 +140,23 @@ def run_encode(args) -> dict:
     t0 = time.time()
     enc = loadModernBert(be, cfg, lambda nm: HostTensor("f16", W[nm[8:]].shape, W[nm[8:]])
                          if nm.startswith("encoder.") and nm[8:] in W else None, dtype="f16")
-    inp = enc.uploadInputs(ids, valid, B, T)
+    # one batch per step, all resident before anything is timed: every step
+    # encodes new inputs, so it also summarises its own attention masks
+    batches = make_batches(args.warmup + 2 * args.steps, B, T, seed=1)
+    inputs = [enc.uploadInputs(ids, valid, B, T) for ids, valid in batches]
     be.flush()
-    log(f"weights + inputs resident in {time.time() - t0:.1f}s")
+    log(f"weights + {len(inputs)} batches of inputs resident in {time.time() - t0:.1f}s")
+    cursor = iter(range(len(inputs)))
 
     def step():
-        y = enc.encode(inp)
-        return y
+        i = next(cursor)
+        y = enc.encode(inputs[i])
+        be.flush(y, wait=False)  # the whole forward, final LayerNorm included, is launched inside the step
+        be.dispose(y)
+        return i
 
     for _ in range(args.warmup):
-        be.dispose(step())
+        step()
     be.flush()
 
     def timed(n):
@@ -143,23 +164,22 @@ def run_encode(args) -> dict:
         be.flush()
         wall0 = time.perf_counter()
         be.record(ev0)
-        for _ in range(n):
-            be.dispose(step())
+        used = [step() for _ in range(n)]
         be.record(ev1)
         be.flush()
-        return be.elapsed_ms(ev0, ev1), time.perf_counter() - wall0
+        return be.elapsed_ms(ev0, ev1), time.perf_counter() - wall0, used
 
-    gpu_ms, wall = timed(args.steps)
+    gpu_ms, wall, used = timed(args.steps)
     ms_per_step = gpu_ms / args.steps
     tokens = B * T
-    valid_tokens = int(valid.sum())
-    log(f"timed {args.steps} steps: {gpu_ms:.2f} ms on the stream ({wall * 1e3:.2f} ms wall) "
+    valid_tokens = float(np.mean([batches[i][1].sum() for i in used]))
+    log(f"timed {args.steps} steps (one new batch each): {gpu_ms:.2f} ms on the stream ({wall * 1e3:.2f} ms wall) "
         f"-> {ms_per_step:.3f} ms/step")
 
     # second timed region: HIP events around every linear launch (on the
     # backend's stream) -> per-launch GPU time by shape
     be.startProfiling(only={"hb_linear"})
-    gpu_ms2, _ = timed(args.steps)
+    gpu_ms2, _, _ = timed(args.steps)
     prof = be.stopProfiling()
     log(f"instrumented region: {gpu_ms2 / args.steps:.3f} ms/step")
     dom = {k: v for k, v in prof.items() if _is_dominant(k)}
@@ -177,19 +197,43 @@ def run_encode(args) -> dict:
     log(f"dominant kernel: {dom_n // args.steps} launches/forward, avg {dom_ms / dom_n * 1e3:.1f} us, "
         f"{achieved:.1f} TFLOP/s")
     traffic = _profiled_traffic()
+    for inp in inputs:
+        enc.disposeInputs(inp)
 
-    # host-to-host rate (ids and mask uploaded, output read back): never `value`
-    be.dispose(step())
-    be.flush()
+    # host-to-host rate, never `value`: host mask build, uploads over PCIe,
+    # the encode, and the [B, T, 768] f16 output read back; each part timed
+    ids, valid = batches[0]
+    parts = {"masks_ms": 0.0, "upload_ms": 0.0, "encode_ms": 0.0, "read_ms": 0.0}
+    reps = 3
+    from laya_hip.modernbert import attentionMasks
     w0 = time.perf_counter()
-    for _ in range(3):
-        inp2 = enc.uploadInputs(ids, valid, B, T)
-        out = be.read(enc.encode(inp2))
+    for _ in range(reps):
+        a = time.perf_counter()
+        attentionMasks(valid, B, T, cfg.localAttention)
+        parts["masks_ms"] += time.perf_counter() - a
+        a = time.perf_counter()
+        inp2 = enc.uploadInputs(ids, valid, B, T)  # builds the masks again, then uploads
+        be.flush()
+        parts["upload_ms"] += time.perf_counter() - a
+        a = time.perf_counter()
+        y = enc.encode(inp2)
+        be.flush(y)
+        parts["encode_ms"] += time.perf_counter() - a
+        a = time.perf_counter()
+        out = be.read(y)
+        parts["read_ms"] += time.perf_counter() - a
+        be.dispose(y)
         enc.disposeInputs(inp2)
-    pcie_ms = (time.perf_counter() - w0) / 3 * 1e3
-    log(f"host-to-host (upload ids/mask, encode, read [{B},{T},768] f16 back): {pcie_ms:.2f} ms/step")
+    pcie_ms = (time.perf_counter() - w0) / reps * 1e3
+    parts = {k: v / reps * 1e3 for k, v in parts.items()}
+    parts["upload_ms"] -= parts["masks_ms"]  # uploadInputs' own mask build
+    log(f"host-to-host (build masks, upload ids/masks, encode, read [{B},{T},768] f16 back): {pcie_ms:.2f} ms/step "
+        f"= " + ", ".join(f"{k} {v:.2f}" for k, v in parts.items()))
 
-    out = be.read(step())
+    inp = enc.uploadInputs(ids, valid, B, T)
+    y = enc.encode(inp)
+    out = be.read(y)
+    be.dispose(y)
     finite = bool(np.isfinite(out.data.astype(np.float32)).all())
     enc.disposeInputs(inp)
     enc.dispose()
@@ -219,7 +263,7 @@ def run_encode(args) -> dict:
             "linear_tflops": lin_flops / (lin_ms * 1e-3) / 1e12,
             "linear_mfma_util_pct": 100.0 * lin_flops / (lin_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS,
             "output_finite": finite, "device": info.get("name") or info.get("arch"),
-            "host_to_host_ms_per_step": pcie_ms,
+            "host_to_host_ms_per_step": pcie_ms, "host_to_host_parts_ms": parts,
         },
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,

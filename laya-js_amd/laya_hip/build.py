@@ -24,8 +24,18 @@ CFLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def _compile(src: str) -> str:
+def _stale(src: str, obj: str) -> bool:
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [src, os.path.join(CSRC, "common.h"), os.path.join(os.path.dirname(ROOT), "include", "laya_hip.h")]
+    return any(os.path.getmtime(d) > t for d in deps if os.path.exists(d))
+
+
+def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(OUT_DIR, os.path.basename(src).replace(".hip", ".o"))
+    if incremental and not _stale(src, obj):
+        return obj
     cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -34,12 +44,14 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 8) -> str:
-    """Compiles every csrc/*.hip and links libhipbackend.so; returns its path."""
+def build(jobs: int = 8, incremental: bool = False) -> str:
+    """Compiles every csrc/*.hip and links libhipbackend.so; returns its path.
+    `incremental` recompiles only the sources newer than their objects (or
+    than common.h / laya_hip.h)."""
     os.makedirs(OUT_DIR, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda s_: _compile(s_, incremental), srcs))
     tmp = LIB + ".tmp"
     r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp],
                        capture_output=True, text=True)
@@ -50,4 +62,5 @@ def build(jobs: int = 8) -> str:
 
 
 if __name__ == "__main__":
-    print(build())
+    import sys
+    print(build(incremental="--incremental" in sys.argv))
