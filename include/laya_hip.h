@@ -261,6 +261,20 @@ int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, 
 int hb_sdpa_panel(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks, uintptr_t v,
                   const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info, uintptr_t o, int64_t B,
                   int64_t H, int64_t Lq, int64_t Lk, int64_t D, float scale, double rope_q, double rope_k);
+/* hb_sdpa without RoPE (rope_q = rope_k = 0) that allocates nothing: no
+ * hipMalloc, no pool block.  No counterpart in the reference; it is for
+ * callers that cannot allocate (code recorded into a HIP graph, tight
+ * serving loops, harnesses that forbid allocation).  With a mask on the MFMA
+ * path, the mask summary is built into a 2 MiB device array the library
+ * holds per GPU until the process ends, so B * ceil(Lq/128) * ceil(Lk/64)
+ * * 8 must not exceed 2097152 bytes (B = 32 at Lq = Lk = 8192); larger
+ * shapes are refused with an error before anything is launched.  Every
+ * call on one GPU shares that array: calls that overlap on one GPU (from
+ * contexts with different streams) race; calls on one context's stream are
+ * ordered.  Results are hb_sdpa's, bit for bit. */
+int hb_sdpa_noalloc(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
+                    uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t o, const int64_t* os,
+                    int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, float scale);
 /* Size of a mask summary for (B, Lq, Lk). */
 int hb_sdpa_mask_info_bytes(int64_t B, int64_t Lq, int64_t Lk, size_t* bytes);
 /* Summarises a bool attention mask (strides ms[4] over [B,H,Lq,Lk], head

@@ -21,9 +21,20 @@
 // projection, in the panel order of the GEMM's X operand.
 //
 // sdpa_simt: the f32 path and the fallback for other head dims / layouts.
+//
+// hb_sdpa_noalloc: hb_sdpa without RoPE for callers that cannot allocate; its
+// mask summary goes to `scratch`, a file-scope device array.
+#include <mutex>
 #include <stdexcept>
 
 #include "common.h"
+
+// Scratch of hb_sdpa_noalloc: the mask summary (one byte per 16-query group
+// of every 128-query x 64-key tile), for B * ceil(Lq/128) * ceil(Lk/64) <=
+// 262144 tiles (B = 32 at Lq = Lk = 8192).  Every GPU the library runs on
+// holds its own copy until the process ends.
+constexpr size_t kSdpaScratchBytes = (size_t)2 << 20;
+static __device__ __align__(256) uint8_t scratch[kSdpaScratchBytes];
 
 namespace hb {
 
@@ -687,6 +698,55 @@ static void sdpa_impl(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uin
                                      tq, tk);
     check_launch("hb_sdpa(generic)");
   }
+}
+
+// The device address of `scratch` on each device, found once per device at
+// hb_init (with that device current).  Host code passes these addresses to
+// kernels; the array's name is only a host-side stand-in.
+static std::mutex g_scratch_mu;
+static void* g_scratch[64];
+
+namespace hb {
+void sdpa_scratch_init(int device) {
+  HB_REQUIRE(device >= 0 && device < 64, "sdpa scratch: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[device]) return;
+  void* p = nullptr;
+  HB_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  HB_REQUIRE(p != nullptr, "sdpa scratch: no device address");
+  g_scratch[device] = p;
+}
+}  // namespace hb
+
+extern "C" int hb_sdpa_noalloc(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
+                               uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t o,
+                               const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
+                               float scale) {
+  HB_API_BEGIN
+  HB_REQUIRE(qs && ks && vs && os && (!mask || ms), "hb_sdpa_noalloc: null strides");
+  HB_REQUIRE(B >= 0 && H >= 0 && Lq >= 0 && Lk >= 0 && D > 0 && B < 65536 && H < 65536 && Lq < (1 << 30) &&
+                 Lk < (1 << 30),
+             "hb_sdpa_noalloc: bad shape");
+  uintptr_t info = 0;
+  if (mask && B > 0 && H > 0 && Lq > 0 && Lk > 0) {
+    const size_t need = mask_info_bytes(B, Lq, Lk);
+    HB_REQUIRE(need <= kSdpaScratchBytes,
+               "hb_sdpa_noalloc: the mask summary needs " + std::to_string(need) + " bytes, more than the " +
+                   std::to_string(kSdpaScratchBytes) + "-byte scratch (B * ceil(Lq/128) * ceil(Lk/64) * 8); "
+                   "use hb_sdpa for this shape");
+    void* p;
+    {
+      std::lock_guard<std::mutex> lock(g_scratch_mu);
+      p = g_scratch[device_of(ctx) & 63];
+    }
+    HB_REQUIRE(p, "hb_sdpa_noalloc: scratch not set up for this device (hb_init does it)");
+    // every byte the attention kernel reads is written here: nothing to clear
+    launch_mask_info(stream_of(ctx), (const uint8_t*)mask, s4(ms), B, Lq, Lk, (uint8_t*)p);
+    check_launch("hb_sdpa_noalloc(mask info)");
+    info = (uintptr_t)p;
+  }
+  sdpa_impl(ctx, dt, q, qs, k, ks, v, vs, mask, ms, info, o, os, B, H, Lq, Lk, D, scale, 0.0, 0.0, 0);
+  HB_API_END
 }
 
 extern "C" int hb_sdpa(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,

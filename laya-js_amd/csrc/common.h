@@ -44,6 +44,8 @@ struct Context;
 hipStream_t stream_of(uintptr_t ctx);
 int device_of(uintptr_t ctx);
 int cu_count(uintptr_t ctx);
+// finds the device address of hb_sdpa_noalloc's scratch on `device` (current)
+void sdpa_scratch_init(int device);
 // scratch memory from the context's stream-ordered pool (freed with pool_free)
 void* pool_alloc(uintptr_t ctx, size_t bytes);
 void pool_free(uintptr_t ctx, void* p);

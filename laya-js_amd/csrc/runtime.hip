@@ -226,6 +226,7 @@ int hb_init(int device, uintptr_t* ctx) {
   HB_CHECK_HIP(hipGetDeviceProperties(&prop, device));
   std::string arch = prop.gcnArchName;
   HB_REQUIRE(arch.rfind("gfx950", 0) == 0, "hb_init: libhipbackend is built for gfx950 (MI355X); device is " + arch);
+  sdpa_scratch_init(device);
   Context* c = new Context();
   c->device = device;
   c->cus = prop.multiProcessorCount;

@@ -66,6 +66,7 @@ SYMBOLS: dict[str, tuple] = {
     "hb_rope": (I, [U, I, U, PI64, I, U, I64, I64, I64, I64, D]),
     "hb_sdpa": (I, [U, I, U, PI64, U, PI64, U, PI64, U, PI64, U, U, PI64, I64, I64, I64, I64, I64, F, D, D]),
     "hb_sdpa_panel": (I, [U, I, U, PI64, U, PI64, U, PI64, U, PI64, U, U, I64, I64, I64, I64, I64, F, D, D]),
+    "hb_sdpa_noalloc": (I, [U, I, U, PI64, U, PI64, U, PI64, U, PI64, U, PI64, I64, I64, I64, I64, I64, F]),
     "hb_sdpa_mask_info_bytes": (I, [I64, I64, I64, C.POINTER(C.c_size_t)]),
     "hb_sdpa_mask_info": (I, [U, U, PI64, I64, I64, I64, U]),
     "hb_geglu": (I, [U, I, U, I64, I, U, I64, I64]),
