@@ -1,0 +1,910 @@
+// MFMA GEMM kernels and their launchers (templates), shared by the
+// translation units that instantiate them by weight format: gemm_f16.hip
+// (16-bit weights), gemm_q8.hip and gemm_q4.hip (laya's quantized format);
+// gemm.hip holds the entry points, the SIMT kernels and the dispatch.
+#pragma once
+#include <atomic>
+#include <stdexcept>
+#include <type_traits>
+
+#include "common.h"
+
+namespace hb {
+
+
+// ------------------------------------------------------------------ helpers
+
+
+template <bool BF16>
+__device__ __forceinline__ float16v mfma32(const uint4v& a, const uint4v& b, float16v c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                  0, 0);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float to_f(uint32_t h) {
+  return BF16 ? bf16_to_f32((uint16_t)h) : f16_bits_to_f32((uint16_t)h);
+}
+template <bool BF16>
+__device__ __forceinline__ uint16_t from_f(float v) {
+  return BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+}
+
+// LDS element offset of 16-byte chunk c of row r in a [rows][64] u16 tile.
+__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+
+// Tile index for block `bid` of `nb`: contiguous runs of tiles per XCD.
+__device__ __forceinline__ int xcd_tile(int bid, int nb) {
+  int xcd = bid & 7, idx = bid >> 3;
+  int q = nb >> 3, rem = nb & 7;
+  return xcd * q + (xcd < rem ? xcd : rem) + idx;
+}
+
+// Quantized code e (0..7) of a chunk: q8 codes are bytes of (w0, w1), q4
+// codes nibbles of w0 (even column in the low nibble).
+template <int QB, bool AFF>
+__device__ __forceinline__ int qcode(uint32_t w0, uint32_t w1, int e) {
+  if constexpr (QB == 8) {
+    uint32_t w = e < 4 ? w0 : w1;
+    int sh = 8 * (e & 3);
+    return AFF ? (int)((w >> sh) & 0xff) : (int)(int8_t)((w >> sh) & 0xff);
+  } else {
+    int v = (int)((w0 >> (4 * e)) & 0xf);
+    return AFF ? v : ((v ^ 8) - 8);
+  }
+}
+
+// 8 dequantized weights as 16-bit values.  f16 with f16 scales: one f16 fma
+// (q is exact in f16), so the weight is fl16(q*s + z) rounded once.  Other
+// combinations compute in f32 and round once to the storage type.
+template <int QB, bool AFF, bool SF32, bool BF16>
+__device__ __forceinline__ uint4v dequant8(uint32_t w0, uint32_t w1, uint32_t sbits, uint32_t zbits, float sf,
+                                           float zf) {
+  uint32_t out[4];
+  if constexpr (!SF32 && !BF16) {
+    f16 s, z;
+    uint16_t sb = (uint16_t)sbits, zb = (uint16_t)zbits;
+    __builtin_memcpy(&s, &sb, 2);
+    __builtin_memcpy(&z, &zb, 2);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      f16 q0 = (f16)(float)qcode<QB, AFF>(w0, w1, e), q1 = (f16)(float)qcode<QB, AFF>(w0, w1, e + 1);
+      f16 r0 = AFF ? __builtin_fmaf16(q0, s, z) : (f16)(q0 * s);
+      f16 r1 = AFF ? __builtin_fmaf16(q1, s, z) : (f16)(q1 * s);
+      uint16_t b0, b1;
+      __builtin_memcpy(&b0, &r0, 2);
+      __builtin_memcpy(&b1, &r1, 2);
+      out[e >> 1] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+    }
+  } else {
+    const float s = SF32 ? sf : f16_bits_to_f32((uint16_t)sbits);
+    const float z = SF32 ? zf : f16_bits_to_f32((uint16_t)zbits);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float q0 = (float)qcode<QB, AFF>(w0, w1, e), q1 = (float)qcode<QB, AFF>(w0, w1, e + 1);
+      float r0 = AFF ? fmaf(q0, s, z) : q0 * s;
+      float r1 = AFF ? fmaf(q1, s, z) : q1 * s;
+      out[e >> 1] = (uint32_t)from_f<BF16>(r0) | ((uint32_t)from_f<BF16>(r1) << 16);
+    }
+  }
+  return uint4v{out[0], out[1], out[2], out[3]};
+}
+
+struct QW {  // quantized weight operand
+  const uint8_t* q;
+  const void* scales;
+  const void* zeros;
+  int G;      // groups per row
+  int group;  // values per group
+};
+
+// Copies a [BM][BNO] 16-bit tile staged in LDS to Y with 16-byte coalesced
+// stores; with a residual, y = round(tile + resid) (linear, then add).
+template <bool BF16, int BM, int BNO, int NT>
+__device__ __forceinline__ void write_tile(const uint16_t* Cs, int m0, int n0, int M, int N,
+                                           const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
+                                           int64_t ldy) {
+  constexpr int CPR = BNO / 8;  // chunks per row
+  for (int q = threadIdx.x; q < BM * CPR; q += NT) {
+    const int r = q / CPR, c = q % CPR;
+    const int gm = m0 + r, gn = n0 + c * 8;
+    if (gm >= M || gn >= N) continue;
+    uint4v v = *(const uint4v*)(Cs + r * BNO + c * 8);
+    if (gn + 8 <= N) {
+      if (R != nullptr) {
+        uint4v rv = *(const uint4v*)(R + (int64_t)gm * ldr + gn);
+        uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t rr[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          uint16_t lo = from_f<BF16>(to_f<BF16>(vv[e] & 0xffff) + to_f<BF16>(rr[e] & 0xffff));
+          uint16_t hi = from_f<BF16>(to_f<BF16>(vv[e] >> 16) + to_f<BF16>(rr[e] >> 16));
+          vv[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        v = uint4v{vv[0], vv[1], vv[2], vv[3]};
+      }
+      *(uint4v*)(Y + (int64_t)gm * ldy + gn) = v;
+    } else {
+      uint16_t vs[8];
+      __builtin_memcpy(vs, &v, 16);
+      for (int e = 0; e < 8 && gn + e < N; e++) {
+        uint16_t o = vs[e];
+        if (R != nullptr) o = from_f<BF16>(to_f<BF16>(o) + to_f<BF16>(R[(int64_t)gm * ldr + gn + e]));
+        Y[(int64_t)gm * ldy + gn + e] = o;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ MFMA kernel
+
+template <int BM, int BN, int WM, int WN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restrict__ X, int64_t ldx,
+                                                         const uint16_t* __restrict__ W, QW qw,
+                                                         const uint16_t* __restrict__ bias,
+                                                         const uint16_t* __restrict__ R, int64_t ldr,
+                                                         uint16_t* __restrict__ Y, int64_t ldy, int M, int N, int K,
+                                                         int tiles_n) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int BK = 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 blocks per wave
+  constexpr int A_LD = BM * 8 / NT, B_LD = BN * 8 / NT;
+  constexpr int BNO = GEGLU ? BN / 2 : BN;  // output columns per tile
+  static_assert(A_LD * NT == BM * 8 && B_LD * NT == BN * 8, "tile/threads mismatch");
+  static_assert(!GEGLU || (TN % 2 == 0), "GEGLU needs an even number of column blocks per wave");
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* As = smem;                // [2][BM*64]
+  uint16_t* Bs = smem + 2 * BM * BK;  // [2][BN*64]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int m0 = (tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BNO;  // first output column (pair index for GEGLU)
+
+  // B tile row r -> W row (GEGLU: first half value rows, second half gate rows)
+  auto w_row = [&](int r) -> int {
+    if constexpr (GEGLU) return r < BN / 2 ? n0 + r : N + n0 + (r - BN / 2);
+    else return n0 + r;
+  };
+  auto w_valid = [&](int r) -> bool {
+    if constexpr (GEGLU) return n0 + (r < BN / 2 ? r : r - BN / 2) < N;
+    else return n0 + r < N;
+  };
+
+  // One K stage in registers on its way to LDS.  16-bit weights: one set, a
+  // stage loaded one stage before it is computed.  Quantized weights: two sets
+  // rotate, a stage loaded two stages ahead, so the loads and the
+  // dequantization behind them have two stages to complete (M = 512, q4:
+  // 29 -> 23 us for Wqkv; the 16-bit kernel measured 1 us slower that way)
+  struct RegSet {
+    uint4v ra[A_LD], rb[B_LD];
+    uint32_t rs[QB ? B_LD : 1], rz[QB ? B_LD : 1];
+    float rsf[QB && SF32 ? B_LD : 1], rzf[QB && SF32 ? B_LD : 1];
+  };
+  auto load_regs = [&](RegSet& R, int k0) __attribute__((always_inline)) {
+    uint4v(&ra)[A_LD] = R.ra;
+    uint4v(&rb)[B_LD] = R.rb;
+    auto& rs = R.rs;
+    auto& rz = R.rz;
+    auto& rsf = R.rsf;
+    auto& rzf = R.rzf;
+#pragma unroll
+    for (int i = 0; i < A_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      int k = k0 + c * 8;
+      if (m0 + r < M && k < K) ra[i] = *(const uint4v*)(X + (int64_t)(m0 + r) * ldx + k);
+      else ra[i] = uint4v{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      int k = k0 + c * 8;
+      bool ok = w_valid(r) && k < K;
+      if constexpr (QB == 0) {
+        rb[i] = ok ? *(const uint4v*)(W + (int64_t)w_row(r) * K + k) : uint4v{0, 0, 0, 0};
+      } else {
+        rb[i] = uint4v{0, 0, 0, 0};
+        rs[i] = rz[i] = 0;
+        if constexpr (SF32) rsf[i] = rzf[i] = 0.f;
+        if (ok) {
+          int64_t row = w_row(r);
+          if constexpr (QB == 8) {
+            uint2v w = *(const uint2v*)(qw.q + row * K + k);
+            rb[i].x = w.x;
+            rb[i].y = w.y;
+          } else {
+            rb[i].x = *(const uint32_t*)(qw.q + row * (K / 2) + k / 2);
+          }
+          int64_t gi = row * qw.G + k / qw.group;
+          if constexpr (SF32) {
+            rsf[i] = ((const float*)qw.scales)[gi];
+            if constexpr (AFF) rzf[i] = ((const float*)qw.zeros)[gi];
+          } else {
+            rs[i] = ((const uint16_t*)qw.scales)[gi];
+            if constexpr (AFF) rz[i] = ((const uint16_t*)qw.zeros)[gi];
+          }
+        }
+      }
+    }
+  };
+  auto store_lds = [&](int buf, const RegSet& R) __attribute__((always_inline)) {
+    const uint4v(&ra)[A_LD] = R.ra;
+    const uint4v(&rb)[B_LD] = R.rb;
+    const auto& rs = R.rs;
+    const auto& rz = R.rz;
+    const auto& rsf = R.rsf;
+    const auto& rzf = R.rzf;
+    uint16_t* a = As + buf * BM * BK;
+    uint16_t* b = Bs + buf * BN * BK;
+#pragma unroll
+    for (int i = 0; i < A_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      *(uint4v*)(a + swz(r, c)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      if constexpr (QB == 0) {
+        *(uint4v*)(b + swz(r, c)) = rb[i];
+      } else {
+        float sf = 0.f, zf = 0.f;
+        if constexpr (SF32) {
+          sf = rsf[i];
+          zf = rzf[i];
+        }
+        *(uint4v*)(b + swz(r, c)) = dequant8<QB, AFF, SF32, BF16>(rb[i].x, rb[i].y, rs[i], rz[i], sf, zf);
+      }
+    }
+  };
+
+  // column block tn of this wave -> tile column (B tile row)
+  auto bcol = [&](int tn) -> int {
+    if constexpr (GEGLU) {
+      constexpr int H = TN / 2;
+      return tn < H ? wn * (WTN / 2) + tn * 32 : BN / 2 + wn * (WTN / 2) + (tn - H) * 32;
+    } else {
+      return wn * WTN + tn * 32;
+    }
+  };
+
+  float16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+  const int l32 = lane & 31, lg = lane >> 5;
+
+  const int KT = (K + BK - 1) / BK;
+  constexpr int AHEAD = QB ? 2 : 1;  // register sets, stages loaded ahead
+  RegSet R0, R1;
+  load_regs(R0, 0);
+  if (AHEAD == 2 && KT > 1) load_regs(R1, BK);
+  store_lds(0, R0);
+  __syncthreads();
+  // stage kt: loads stage kt + AHEAD into `rfree` (AHEAD = 2: its previous
+  // stage is in LDS already; AHEAD = 1: rfree is rnext), computes stage kt
+  // from LDS, stages kt + 1 (held in `rnext`) into the other LDS buffer
+  auto stage = [&](int kt, RegSet& rnext, RegSet& rfree) __attribute__((always_inline)) {
+    const int buf = kt & 1;
+    if (kt + AHEAD < KT) load_regs(rfree, (kt + AHEAD) * BK);
+    const uint16_t* a = As + buf * BM * BK;
+    const uint16_t* b = Bs + buf * BN * BK;
+    // k16 substeps in increasing k; W rows as the A operand and X rows as
+    // the B operand, the order the large-M kernel uses, so both kernels
+    // produce the same bits for a row whatever M is
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const int c = 2 * s + lg;
+      uint4v af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) af[i] = *(const uint4v*)(a + swz(wm * WTM + i * 32 + l32, c));
+#pragma unroll
+      for (int j = 0; j < TN; j++) bf[j] = *(const uint4v*)(b + swz(bcol(j) + l32, c));
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = mfma32<BF16>(bf[j], af[i], acc[i][j]);
+    }
+    if (kt + 1 < KT) store_lds(buf ^ 1, rnext);
+    __syncthreads();
+  };
+  if constexpr (AHEAD == 2) {
+    for (int kt = 0; kt < KT; kt += 2) {
+      stage(kt, R1, R0);
+      if (kt + 1 < KT) stage(kt + 1, R0, R1);
+    }
+  } else {
+    for (int kt = 0; kt < KT; kt++) stage(kt, R0, R0);
+  }
+
+  // ---- epilogue: bias, one rounding, GeGLU, stage in LDS as [BM][BNO];
+  // lane l holds row l % 32 and columns 8*(r/4) + 4*(l/32) + {0..3}
+  uint16_t* Cs = smem;
+  constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
+  constexpr int WTNO = GEGLU ? WTN / 2 : WTN;
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    const int orow = wm * WTM + i * 32 + l32;
+#pragma unroll
+    for (int j = 0; j < OUT_TN; j++) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int ocol = wn * WTNO + j * 32 + 8 * g + 4 * lg;  // tile output column of element 0
+        uint16_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int gcol = n0 + ocol + e;
+          float bv = 0.f, bg = 0.f;
+          if (bias != nullptr && gcol < N) {
+            bv = to_f<BF16>(bias[gcol]);
+            if constexpr (GEGLU) bg = to_f<BF16>(bias[N + gcol]);
+          }
+          float v = to_f<BF16>(from_f<BF16>(acc[i][j][4 * g + e] + bv));
+          if constexpr (GEGLU) {
+            const float gt = to_f<BF16>(from_f<BF16>(acc[i][j + TN / 2][4 * g + e] + bg));
+            v = pin_f32(gelu_fast(v) * gt);  // the f32 product, then one rounding to the storage type
+          }
+          o[e] = from_f<BF16>(v);
+        }
+        *(uint2v*)(Cs + orow * BNO + ocol) =
+            uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+      }
+    }
+  }
+  __syncthreads();
+
+  write_tile<BF16, BM, BNO, NT>(Cs, m0, n0, M, N, R, ldr, Y, ldy);
+}
+
+// ------------------------------------------------------------------ large-M MFMA kernel
+
+
+// Persistent GEMM over 256 x BN output tiles.  Four waves are stacked along
+// M: each wave owns 64 rows and every column of the tile as 2 x (BN/32)
+// blocks of v_mfma_f32_32x32x16 (on gfx950 the 32x32 MFMA runs at twice the
+// rate of the 16x16x32 one, and reaches it from a single wave per SIMD).
+// A wave's A rows are private, so they go from global memory straight into
+// MFMA operand registers; only the weight tile is shared, through
+// double-buffered LDS.
+//
+// One block per CU walks a list of tiles as one continuous stream of
+// 64-wide K stages: loads run two stages ahead (three A and two W register
+// sets rotating by name, issued between the MFMAs) and cross tile
+// boundaries, so the next tile's first stages arrive while the current tile
+// finishes.  Blocks on one XCD (block b runs on XCD b % 8) take consecutive
+// tiles, which share A rows in that XCD's L2.
+//
+// The MFMA computes the transposed product (W rows as the A operand, X rows
+// as the B operand): lane l then holds output row l % 32 and the four
+// consecutive columns 8*(r/4) + 4*(l/32) + {0..3} of each accumulator, so the
+// epilogue writes 8-byte pieces of Y straight from registers.
+template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_mfma_arow(
+    const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W, QW qw,
+    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
+    int64_t ldy, int M, int N, int K, int tiles_n, int tiles, int xpan, int ypan) {
+  constexpr int NT = 256, BM = 256, BK = 64;
+  constexpr int TM = 2, TN = BN / 32;  // 32x32 blocks per wave
+  constexpr int KS = BK / 16;          // k16 substeps per stage
+  constexpr int B_LD = BN * 8 / NT;
+  constexpr int BNO = GEGLU ? BN / 2 : BN;
+  static_assert(B_LD * NT == BN * 8 && BN % 32 == 0, "BN must be a multiple of 32");
+  static_assert(!GEGLU || (TN % 2 == 0), "GEGLU needs an even number of column blocks");
+  static_assert((BM * (BNO / 8)) % NT == 0, "write-out assumes whole rounds of chunks");
+
+  constexpr int CPR = BNO / 8;           // 16-byte chunks per output row
+  constexpr int RG = (CPR + 7) / 8;      // C tile: groups of 8 chunks per row
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* Bs = smem;               // [2][BN*64] W tiles
+  uint16_t* Cs = smem + 2 * BN * BK;  // [RG][BM][8] 16-byte chunks: residual in, output out
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, lg = lane >> 5;
+
+  // This block's tiles (gridDim.x % 8 == 0).  XCD x owns the row panels
+  // [mb0, mb1) with every column tile, and its blocks take the panel's tiles
+  // column-tile-major: local tile l = slot + i * nx is row panel mb0 + l % mx,
+  // column tile l / mx.  The tiles one XCD computes at a time then share a
+  // few column tiles of W and cycle over the XCD's own rows of X, which stay
+  // in its L2 from one column tile to the next.
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, nx = gridDim.x >> 3;
+  const int tiles_m = tiles / tiles_n;
+  const int mb0 = xcd * tiles_m / 8, mx = (xcd + 1) * tiles_m / 8 - mb0;
+  const int nloc = mx * tiles_n;
+  const int ntile = nloc > slot ? (nloc - slot + nx - 1) / nx : 0;
+  if (ntile == 0) return;
+  const int KT = (K + BK - 1) / BK;
+  const int S = ntile * KT;  // stages in this block's stream
+  auto tile_m0 = [&](int i) { return (mb0 + (slot + i * nx) % mx) * BM; };
+  auto tile_n0 = [&](int i) { return ((slot + i * nx) / mx) * BNO; };
+
+  // X is row-major (x[row * ldx + k]) or in panel order (xpan; 32-row x
+  // 16-column blocks of 1 KB in MFMA operand order, rows padded to a multiple
+  // of 32).  For k % 8 == 0 both are x[xs_hi * (row / 32) + xs_lo * (row % 32)
+  // + xk * k]; in panel order one fragment load then reads one whole block.
+  const int64_t xs_hi = xpan ? (int64_t)32 * K : (int64_t)32 * ldx;
+  const int64_t xs_lo = xpan ? 8 : ldx;
+  const int xk = xpan ? 32 : 1;
+  const int mlim = xpan ? ((M + 31) & ~31) : M;
+  // Loads are branch-free: addresses are clamped into the operand.  Rows past
+  // M (A) or N (W) only feed outputs that are never stored, so they need no
+  // zeroing; a K tail (K % 64 != 0, KTAIL, row-major X only) is zeroed.
+  auto load_a = [&](int m0, int k0, uint4v (&a)[TM][KS]) {
+    const int arow = m0 + wave * 64 + l32;
+#pragma unroll
+    for (int rb = 0; rb < TM; rb++)
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        const int row = arow + rb * 32, k = k0 + s * 16 + lg * 8;
+        const int rc = row < mlim ? row : mlim - 1;
+        const uint4v v = *(const uint4v*)(X + (int64_t)(rc >> 5) * xs_hi + (int64_t)(rc & 31) * xs_lo +
+                                          (int64_t)xk * (KTAIL && k >= K ? 0 : k));
+        a[rb][s] = (KTAIL && k >= K) ? uint4v{0, 0, 0, 0} : v;
+      }
+  };
+
+  struct BRegs {
+    uint4v v[B_LD];
+    uint32_t s[QB ? B_LD : 1], z[QB ? B_LD : 1];
+    float sf[QB && SF32 ? B_LD : 1], zf[QB && SF32 ? B_LD : 1];
+  };
+  // B tile row r -> W row (GEGLU: first half value rows, second half gate rows)
+  auto load_b = [&](int n0, int k0, BRegs& br) {
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      const int q = tid + i * NT, r = q >> 3, c = q & 7;
+      const int k = k0 + c * 8;
+      const int nn = GEGLU ? n0 + (r < BN / 2 ? r : r - BN / 2) : n0 + r;
+      const bool rv = nn < N;
+      const int wr = GEGLU && r >= BN / 2 ? N + nn : nn;
+      if constexpr (QB == 0) {
+        const uint4v v = *(const uint4v*)(W + (int64_t)(rv ? wr : 0) * K + (KTAIL && k >= K ? 0 : k));
+        br.v[i] = (KTAIL && k >= K) ? uint4v{0, 0, 0, 0} : v;
+      } else {
+        br.v[i] = uint4v{0, 0, 0, 0};
+        br.s[i] = br.z[i] = 0;
+        if constexpr (SF32) br.sf[i] = br.zf[i] = 0.f;
+        if (rv && k < K) {
+          const int64_t row = wr;
+          if constexpr (QB == 8) {
+            uint2v w = *(const uint2v*)(qw.q + row * K + k);
+            br.v[i].x = w.x;
+            br.v[i].y = w.y;
+          } else {
+            br.v[i].x = *(const uint32_t*)(qw.q + row * (K / 2) + k / 2);
+          }
+          const int64_t gi = row * qw.G + k / qw.group;
+          if constexpr (SF32) {
+            br.sf[i] = ((const float*)qw.scales)[gi];
+            if constexpr (AFF) br.zf[i] = ((const float*)qw.zeros)[gi];
+          } else {
+            br.s[i] = ((const uint16_t*)qw.scales)[gi];
+            if constexpr (AFF) br.z[i] = ((const uint16_t*)qw.zeros)[gi];
+          }
+        }
+      }
+    }
+  };
+  auto store_b = [&](int buf, const BRegs& br) {
+    uint16_t* b = Bs + buf * BN * BK;
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      int q = tid + i * NT, r = q >> 3, c = q & 7;
+      if constexpr (QB == 0) {
+        *(uint4v*)(b + swz(r, c)) = br.v[i];
+      } else {
+        float sf = 0.f, zf = 0.f;
+        if constexpr (SF32) {
+          sf = br.sf[i];
+          zf = br.zf[i];
+        }
+        *(uint4v*)(b + swz(r, c)) = dequant8<QB, AFF, SF32, BF16>(br.v[i].x, br.v[i].y, br.s[i], br.z[i], sf, zf);
+      }
+    }
+  };
+  // column block j of the tile -> W tile row (GEGLU: value blocks, then gate blocks)
+  auto bcol = [&](int j) -> int {
+    if constexpr (GEGLU) return j < TN / 2 ? j * 32 : BN / 2 + (j - TN / 2) * 32;
+    else return j * 32;
+  };
+
+  // The C tile in LDS: 16-byte chunk c of tile row r sits in slot
+  // (c/8)*BM*8 + r*8 + ((c%8) ^ (r%8)).  The epilogue's 8-byte accesses of 32
+  // consecutive rows then spread over the banks, and 8 consecutive chunks of
+  // a row are 8 distinct slots of one 128-byte span.  With a residual the
+  // tile is first filled with R straight from global memory
+  // (global_load_lds_dwordx4, issued at the tile's first K stage); the
+  // epilogue adds the rounded linear output in place, and the whole tile
+  // leaves with coalesced 16-byte stores (whole rows per instruction: partial
+  // lines written from registers cost HBM write-backs twice over).
+  auto r_slot = [&](int r, int c) { return (c >> 3) * (BM * 8) + r * 8 + ((c & 7) ^ (r & 7)); };
+  // DMA instruction i of wave w fills slots (4i + w)*64 + lane, i.e. row
+  // 32*(i%8) + 8w + lane/8, chunk 8*(i/8) + ((lane%8) ^ (lane/8)).  Every lane
+  // writes its own slot, so slots outside the operand load a clamped,
+  // in-bounds address (ldr % 8 == 0: a chunk starting below N lies inside the
+  // row) and are never stored.
+  auto dma_resid = [&](int m0, int n0) {
+    int ln = lane, wv = wave;
+    asm volatile("" : "+v"(ln), "+v"(wv));  // per-tile address math, not hoisted (see the epilogue)
+    const int r_cx = (ln & 7) ^ (ln >> 3);
+    const int rbase = m0 + wv * 8 + (ln >> 3), cbase = n0 + r_cx * 8;
+#pragma unroll
+    for (int i = 0; i < RG * 8; i++) {
+      const int row = rbase + (i & 7) * 32, col = cbase + (i >> 3) * 64;
+      const bool cok = (i >> 3) * 8 + r_cx < CPR && col < N;
+      __builtin_amdgcn_global_load_lds((const void*)(R + (int64_t)(row < M ? row : M - 1) * ldr + (cok ? col : 0)),
+                                       (__attribute__((address_space(3))) void*)(Cs + (i * 4 + wv) * 512), 16, 0,
+                                       0);
+    }
+  };
+
+  float16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  // ---- epilogue: bias, one rounding to the storage type, GeGLU (value
+  // block j and gate block j + TN/2 hold the same output columns), then the
+  // residual add, y = round(round(x.w^T + b) + r), into the C tile
+  constexpr int OUT_TN = GEGLU ? TN / 2 : TN;
+  // The lane indices are re-read through an empty asm inside the epilogue,
+  // the write-out and the residual DMA: the compiler then computes their
+  // per-lane addresses there, once per tile, instead of hoisting all of them
+  // out of the tile loop and spilling them to scratch (an HBM write per
+  // spilled register).
+  auto epilogue = [&](int n0, auto has_bias, auto has_r) {
+    constexpr bool HB = decltype(has_bias)::value, HR = decltype(has_r)::value;
+    int l32 = lane & 31, lg = lane >> 5, wv = wave;
+    asm volatile("" : "+v"(l32), "+v"(lg), "+v"(wv));
+#pragma unroll
+    for (int j = 0; j < OUT_TN; j++) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int col = j * 32 + 8 * g + 4 * lg;  // tile output column of element 0
+        float bv[4] = {0.f, 0.f, 0.f, 0.f}, bg[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (HB) {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (n0 + col + e < N) {
+              bv[e] = to_f<BF16>(bias[n0 + col + e]);
+              if constexpr (GEGLU) bg[e] = to_f<BF16>(bias[N + n0 + col + e]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          uint16_t o[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float a = HB ? acc[i][j][4 * g + e] + bv[e] : acc[i][j][4 * g + e];
+            if constexpr (GEGLU) {
+              const float ag = HB ? acc[i][j + TN / 2][4 * g + e] + bg[e] : acc[i][j + TN / 2][4 * g + e];
+              o[e] = from_f<BF16>(pin_f32(gelu_fast(to_f<BF16>(from_f<BF16>(a))) * to_f<BF16>(from_f<BF16>(ag))));
+            } else {
+              o[e] = from_f<BF16>(a);
+            }
+          }
+          uint2v* cp = (uint2v*)(Cs + r_slot(wv * 64 + i * 32 + l32, col >> 3) * 8 + (col & 7));
+          if constexpr (HR) {
+            const uint2v rv = *cp;
+            const uint16_t rr[4] = {(uint16_t)(rv.x & 0xffff), (uint16_t)(rv.x >> 16), (uint16_t)(rv.y & 0xffff),
+                                    (uint16_t)(rv.y >> 16)};
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = from_f<BF16>(to_f<BF16>(o[e]) + to_f<BF16>(rr[e]));
+          }
+          *cp = uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+        }
+      }
+    }
+  };
+  // the C tile -> Y: thread t takes chunks t, t + 256, ...; consecutive
+  // threads cover consecutive 16-byte pieces of a row (row-major Y) or of a
+  // 1 KB block (panel-order Y, ypan: chunk q is row 32 * rb + q % 32, column
+  // chunk 2 * nb + (q / 32) % 2 with (rb, nb) = divmod(q / 64, CPR / 2))
+  static_assert(CPR % 2 == 0, "panel-order output needs whole 16-column blocks");
+  const int yblk = (N + 15) >> 4;  // 16-column blocks per panel-order row block
+  auto panel_chunk = [&](int q, int& r, int& c) -> int64_t {
+    const int r32 = q & 31, h = (q >> 5) & 1, rest = q >> 6, rb = rest / (CPR / 2), nb = rest - rb * (CPR / 2);
+    r = rb * 32 + r32;
+    c = nb * 2 + h;
+    return ((int64_t)rb * yblk + nb) * 512 + (h * 32 + r32) * 8;  // relative to the tile's first block
+  };
+  // output chunk c of C tile row r
+  auto out_chunk = [&](int r, int c) __attribute__((always_inline)) -> uint4v {
+    return *(const uint4v*)(Cs + r_slot(r, c) * 8);
+  };
+  auto write_out = [&](int m0, int n0) {
+    int t0 = tid;
+    asm volatile("" : "+v"(t0));
+    if (ypan) {
+      uint16_t* yb = Y + ((int64_t)(m0 >> 5) * yblk + (n0 >> 4)) * 512;
+      const int rbl = ((M + 31) >> 5) - (m0 >> 5);  // row blocks of the padded output left from m0
+      for (int q = t0; q < BM * CPR; q += NT) {
+        int r, c;
+        const int64_t o = panel_chunk(q, r, c);
+        if ((r >> 5) >= rbl || n0 + c * 8 >= N) continue;
+        *(uint4v*)(yb + o) = out_chunk(r, c);
+      }
+      return;
+    }
+    if (m0 + BM <= M && n0 + BNO <= N) {  // interior tile: no bounds checks
+      uint16_t* yb = Y + (int64_t)m0 * ldy + n0;
+#pragma unroll
+      for (int k = 0; k < BM * CPR / NT; k++) {
+        const int q = t0 + k * NT, r = q / CPR, c = q - r * CPR;
+        *(uint4v*)(yb + (int64_t)r * ldy + c * 8) = out_chunk(r, c);
+      }
+      return;
+    }
+    for (int q = t0; q < BM * CPR; q += NT) {
+      const int r = q / CPR, c = q - r * CPR;
+      const int gm = m0 + r, gn = n0 + c * 8;
+      if (gm >= M || gn >= N) continue;
+      const uint4v v = out_chunk(r, c);
+      uint16_t* yp = Y + (int64_t)gm * ldy + gn;
+      if (gn + 8 <= N) {
+        *(uint4v*)yp = v;
+      } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        for (int e = 0; gn + e < N; e++) yp[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      }
+    }
+  };
+
+  // Spread write-out: in a block that streams several tiles, an interior
+  // tile's output waits in the C tile and leaves during the first
+  // WO_STAGES stages of the next tile (PER_STAGE 16-byte chunks per thread
+  // and stage) instead of in one burst that every CU issues at the same
+  // moment.  The residual DMA of the next tile then starts at stage
+  // res_stage, after the C tile has drained.
+  constexpr int WO_STAGES = 6, PER_STAGE = BM * CPR / NT / WO_STAGES;
+  static_assert(PER_STAGE * WO_STAGES * NT == BM * CPR, "write-out parts");
+  const bool spread = KT >= 2 * WO_STAGES;
+  const int res_stage = spread ? WO_STAGES : 0;
+  int wo_m0 = -1, wo_n0 = 0, it_cur = 0;  // wo_m0 < 0: no output pending
+  // part `part` (0..WO_STAGES-1) of the pending output; the values are
+  // computed in every tile's first stages (branch-free, between the MFMAs)
+  // and stored only when an output is pending (the block's first tile has
+  // none: its C tile then holds nothing of use)
+  auto write_part = [&](int part) __attribute__((always_inline)) {
+    int t0 = tid;
+    asm volatile("" : "+v"(t0));
+    uint4v v[PER_STAGE];
+    int64_t off[PER_STAGE];
+#pragma unroll
+    for (int k = 0; k < PER_STAGE; k++) {
+      const int q = t0 + (part * PER_STAGE + k) * NT;
+      int r, c;
+      if (ypan) {
+        off[k] = panel_chunk(q, r, c);
+      } else {
+        r = q / CPR;
+        c = q - r * CPR;
+        off[k] = (int64_t)r * ldy + c * 8;
+      }
+      v[k] = out_chunk(r, c);
+    }
+    if (wo_m0 >= 0) {
+      uint16_t* yb = ypan ? Y + ((int64_t)(wo_m0 >> 5) * yblk + (wo_n0 >> 4)) * 512 : Y + (int64_t)wo_m0 * ldy + wo_n0;
+#pragma unroll
+      for (int k = 0; k < PER_STAGE; k++) *(uint4v*)(yb + off[k]) = v[k];
+    }
+  };
+
+  uint4v A0[TM][KS], A1[TM][KS], A2[TM][KS];
+  BRegs B0, B1;
+  // step g: MFMAs on `ac` and LDS buffer g&1; loads stage g+2 of the stream
+  // into (al, bl); stages the W tile of g+1 (held in bs) into the other buffer.
+  // WP: this stage also writes part `kin` of the previous tile's output
+  // (branch-free inside the stage, so the scheduler can put its LDS reads,
+  // VALU work and stores between the MFMAs)
+  auto step = [&](auto wp, int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl,
+                  BRegs& bs) __attribute__((always_inline)) {
+    constexpr bool WP = decltype(wp)::value;
+    // the residual tile arrives while the tile computes, once the previous
+    // tile's output has left the C tile (at once for a block's first tile)
+    if (R != nullptr && kin == (it_cur == 0 ? 0 : res_stage)) dma_resid(tile_m0(it_cur), tile_n0(it_cur));
+    const int g2 = g + 2 < S ? g + 2 : S - 1;
+    const int i2 = g2 / KT, k2 = (g2 - i2 * KT) * BK;
+    load_a(tile_m0(i2), k2, al);
+    load_b(tile_n0(i2), k2, bl);
+    const uint16_t* b = Bs + (g & 1) * BN * BK;
+    uint4v bf[KS][TN];
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) bf[s][j] = *(const uint4v*)(b + swz(bcol(j) + l32, 2 * s + lg));
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) acc[i][j] = mfma32<BF16>(bf[s][j], ac[i][s], acc[i][j]);
+    if constexpr (WP) write_part(kin);
+    // schedule: substep-0 fragment reads, then MFMA pairs, each preceded by
+    // one global load (while any remain) and one fragment read of the next
+    // substep (and, writing out, a share of the VALU work); the W staging for
+    // the next stage goes last
+    constexpr int NVMEM = TM * KS + B_LD, NPAIR = KS * TN;
+    constexpr int NVALU = WP ? 1 : 0;
+    __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
+#pragma unroll
+    for (int p = 0; p < NPAIR; p++) {
+      if (p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (p < (KS - 1) * TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (NVALU) __builtin_amdgcn_sched_group_barrier(0x002, NVALU, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
+    }
+    store_b((g + 1) & 1, bs);
+    __builtin_amdgcn_sched_group_barrier(0x200, B_LD, 0);
+    __syncthreads();
+  };
+
+  {
+    const int m0 = tile_m0(0), n0 = tile_n0(0);
+    const int g1 = S > 1 ? 1 : 0, i1 = g1 / KT, k1 = (g1 - i1 * KT) * BK;
+    load_a(m0, 0, A0);
+    load_b(n0, 0, B0);
+    store_b(0, B0);
+    load_a(tile_m0(i1), k1, A1);
+    load_b(tile_n0(i1), k1, B1);
+    __syncthreads();
+  }
+  // The register rotation has period 6, so a block streams several tiles
+  // only when KT % 6 == 0 (the launcher gives every block one tile otherwise).
+  for (int it = 0; it < ntile; it++) {
+    const int g0 = it * KT;
+    it_cur = it;
+    // six stages (the register rotation's period); with WP, stages 0..5 of
+    // the tile, each writing a sixth of the previous tile's output
+    auto six = [&](auto wp, int kt) __attribute__((always_inline)) {
+      step(wp, g0 + kt, kt, A0, A2, B0, B1);
+      if (kt + 1 < KT) step(wp, g0 + kt + 1, kt + 1, A1, A0, B1, B0);
+      if (kt + 2 < KT) step(wp, g0 + kt + 2, kt + 2, A2, A1, B0, B1);
+      if (kt + 3 < KT) step(wp, g0 + kt + 3, kt + 3, A0, A2, B1, B0);
+      if (kt + 4 < KT) step(wp, g0 + kt + 4, kt + 4, A1, A0, B0, B1);
+      if (kt + 5 < KT) step(wp, g0 + kt + 5, kt + 5, A2, A1, B1, B0);
+    };
+    six(std::true_type{}, 0);  // stages 0..5 write the previous tile's output, if pending
+    wo_m0 = -1;
+    for (int kt = 6; kt < KT; kt += 6) six(std::false_type{}, kt);
+    // the residual DMA (stage res_stage < KT - 1) has landed once at most the
+    // W and A loads of one stage are outstanding (they were all issued after
+    // it, and loads complete in order); the barrier makes every wave's part
+    // of the C tile visible (and, without R, keeps the previous tile's
+    // write-out reads ahead of this epilogue's writes)
+    static_assert(TM * KS + B_LD <= 15, "vmcnt immediate");
+    if (R != nullptr) __builtin_amdgcn_s_waitcnt(0x0F70 | (TM * KS + B_LD));
+    __syncthreads();
+    {
+      using T = std::true_type;
+      using F = std::false_type;
+      const int n0 = tile_n0(it);
+      if (bias == nullptr) {
+        if (R == nullptr) epilogue(n0, F{}, F{});
+        else epilogue(n0, F{}, T{});
+      } else {
+        if (R == nullptr) epilogue(n0, T{}, F{});
+        else epilogue(n0, T{}, T{});
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+    __syncthreads();
+    const int m0 = tile_m0(it), n0 = tile_n0(it);
+    if (spread && it + 1 < ntile && m0 + BM <= M && n0 + BNO <= N) {
+      wo_m0 = m0;  // leaves during the next tile's first stages
+      wo_n0 = n0;
+    } else {
+      write_out(m0, n0);
+      if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
+    }
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+
+template <int BM, int BN, int WM, int WN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
+void launch_mfma(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, QW qw,
+                        const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
+                        int K) {
+  constexpr int BNO = GEGLU ? BN / 2 : BN;
+  int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BNO - 1) / BNO;
+  size_t stage = (size_t)2 * (BM + BN) * 64 * sizeof(uint16_t);
+  size_t ctile = (size_t)BM * BNO * sizeof(uint16_t);
+  size_t lds = stage > ctile ? stage : ctile;
+  auto kern = gemm_mfma<BM, BN, WM, WN, BF16, GEGLU, QB, AFF, SF32>;
+  static std::atomic<uint64_t> attr{0};
+  once_per_device(attr, [&] {
+    HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  });
+  kern<<<tiles_m * tiles_n, WM * WN * 64, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n);
+}
+
+template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
+void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                        QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
+                        int N, int K) {
+  constexpr int BNO = GEGLU ? BN / 2 : BN;
+  const int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO, tiles = tiles_m * tiles_n;
+  // one persistent block per CU, a multiple of 8 (one per XCD); with
+  // K % 384 != 0 at most one tile per block: every XCD gets as many blocks
+  // as the largest XCD share of tiles (ceil(tiles_m / 8) row panels)
+  const int KT = (K + 63) / 64;
+  int grid = KT % 6 == 0 ? (tiles < cus ? tiles : cus) / 8 * 8 : 8 * (((tiles_m + 7) / 8) * tiles_n);
+  HB_REQUIRE(grid >= 8, "hb_linear: large-M GEMM needs at least 8 tiles");
+  constexpr int RG = (BNO / 8 + 7) / 8;
+  const size_t lds = ((size_t)2 * BN * 64 + (size_t)RG * 256 * 64) * sizeof(uint16_t);
+  auto kern = gemm_mfma_arow<BN, BF16, GEGLU, QB, AFF, SF32, KTAIL>;
+  static std::atomic<uint64_t> attr{0};
+  once_per_device(attr, [&] {
+    HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  });
+  kern<<<grid, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n, tiles, (pan & HB_X_PANEL) ? 1 : 0,
+                               (pan & HB_Y_PANEL) ? 1 : 0);
+}
+
+// The large-M kernel runs for M >= 4096; it is the only one that takes
+// panel-order operands (the entry points check that before dispatching).
+inline bool arow_path(int64_t M) { return M >= 4096; }
+
+template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
+void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                          QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
+                          int N, int K) {
+  // large M: persistent 256 x 192 tiles with register-resident A rows; otherwise 128 x 128
+  if (arow_path(M) && K % 64 == 0)
+    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, false>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  else if (arow_path(M))
+    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  else
+    launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+}
+
+template <int QB, bool AFF, bool SF32>
+void mfma_dtype(int dt, bool geglu, hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx,
+                       const uint16_t* w, QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y,
+                       int64_t ldy, int M, int N, int K) {
+  if (dt == HB_F16) {
+    if (geglu) mfma_dispatch<false, true, QB, AFF, SF32>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    else mfma_dispatch<false, false, QB, AFF, SF32>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  } else {
+    if (geglu) mfma_dispatch<true, true, QB, AFF, SF32>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+    else mfma_dispatch<true, false, QB, AFF, SF32>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  }
+}
+
+// Instantiated by gemm_f16.hip (QB = 0), gemm_q8.hip and gemm_q4.hip.
+extern template void mfma_dtype<0, false, false>(int, bool, hipStream_t, int, unsigned, const uint16_t*, int64_t,
+                                                 const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
+                                                 uint16_t*, int64_t, int, int, int);
+extern template void mfma_dtype<8, false, false>(int, bool, hipStream_t, int, unsigned, const uint16_t*, int64_t,
+                                                 const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
+                                                 uint16_t*, int64_t, int, int, int);
+extern template void mfma_dtype<8, true, false>(int, bool, hipStream_t, int, unsigned, const uint16_t*, int64_t,
+                                                const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
+                                                uint16_t*, int64_t, int, int, int);
+extern template void mfma_dtype<4, false, false>(int, bool, hipStream_t, int, unsigned, const uint16_t*, int64_t,
+                                                 const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
+                                                 uint16_t*, int64_t, int, int, int);
+extern template void mfma_dtype<4, true, false>(int, bool, hipStream_t, int, unsigned, const uint16_t*, int64_t,
+                                                const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
+                                                uint16_t*, int64_t, int, int, int);
+
+}  // namespace hb

@@ -1,0 +1,14 @@
+// q4 weights (symmetric and affine): the MFMA GEMM kernels instantiated for these weight formats
+// (the templates live in gemm_kernels.h).
+#include "gemm_kernels.h"
+
+namespace hb {
+
+template void mfma_dtype<4, false, false>(int, bool, hipStream_t, int, unsigned, const uint16_t*, int64_t,
+                                          const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
+                                          uint16_t*, int64_t, int, int, int);
+template void mfma_dtype<4, true, false>(int, bool, hipStream_t, int, unsigned, const uint16_t*, int64_t,
+                                          const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
+                                          uint16_t*, int64_t, int, int, int);
+
+}  // namespace hb

@@ -28,7 +28,7 @@ def _stale(src: str, obj: str) -> bool:
     if not os.path.exists(obj):
         return True
     t = os.path.getmtime(obj)
-    deps = [src, os.path.join(CSRC, "common.h"), os.path.join(os.path.dirname(ROOT), "include", "laya_hip.h")]
+    deps = [src, *glob.glob(os.path.join(CSRC, "*.h")), os.path.join(os.path.dirname(ROOT), "include", "laya_hip.h")]
     return any(os.path.getmtime(d) > t for d in deps if os.path.exists(d))
 
 
@@ -47,7 +47,7 @@ def _compile(src: str, incremental: bool = False) -> str:
 def build(jobs: int = 8, incremental: bool = False) -> str:
     """Compiles every csrc/*.hip and links libhipbackend.so; returns its path.
     `incremental` recompiles only the sources newer than their objects (or
-    than common.h / laya_hip.h)."""
+    than any csrc/*.h or laya_hip.h)."""
     os.makedirs(OUT_DIR, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
