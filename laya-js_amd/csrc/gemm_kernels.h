@@ -3,6 +3,8 @@
 // (16-bit weights), gemm_q8.hip and gemm_q4.hip (laya's quantized format);
 // gemm.hip holds the entry points, the SIMT kernels and the dispatch.
 #pragma once
+#include <math.h>
+
 #include <atomic>
 #include <stdexcept>
 #include <type_traits>
@@ -364,6 +366,150 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
   __syncthreads();
 
   write_tile<BF16, BM, BNO, NT>(Cs, m0, n0, M, N, R, ldr, Y, ldy);
+}
+
+// ------------------------------------------------------------------ small-M MFMA kernel
+
+// Small-M GEMM for 16-bit weights (M < 4096, K % 64 == 0): weight-stationary,
+// one memory round trip.  A block of four waves owns a slab of 32*TN W rows
+// (the output columns n0 .. n0 + 32*TNO, and with GeGLU their gate rows too)
+// and 128 rows of X, one 32-row block per wave.  Everything a wave needs is
+// requested at once before anything is waited for: its X fragments for P k16
+// steps (P = K/16 when that fits in registers), its residual and bias values,
+// and its share of the whole slab, which goes to LDS with direct-to-LDS loads
+// (global_load_lds: 16 bytes per lane, whole 128-byte lines of 8 rows per
+// instruction), so the kernel waits for memory once.  What bounds it is the
+// X fragment loads (32 rows x 32 bytes per 1 KB instruction), which a CU's L1
+// serves at about 15 bytes per clock; the launcher uses the kernel while its
+// blocks fit one per CU (Wqkv at M = 128: 72 blocks, 11 us against 15 us for
+// the 128 x 128 kernel, which ran 18 blocks).
+// The k16 steps then run in ascending order with the same MFMA, operand
+// order (W rows as the A operand, X rows as the B operand) and epilogue as
+// the other kernels, so a row's bits do not depend on M.
+// Slab layout: 1 KB blocks of 8 rows x 64 k, block (r/8)*KB + k/64 (KB = K/64),
+// 16-byte chunk c of row r at slot (r%8)*8 + (c ^ (r%8)), so the 8 lanes of a
+// fragment read that share a row group hit 8 distinct bank groups.  Blocks
+// are numbered row-chunk-fastest and dealt to XCDs in contiguous runs: the
+// blocks that read one slab share an XCD's L2.
+template <int TN, int P, bool BF16, bool GEGLU>
+__global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X, int64_t ldx,
+                                                 const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
+                                                 const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
+                                                 int64_t ldy, int M, int N, int K, int chunks) {
+  constexpr int TNO = GEGLU ? TN / 2 : TN;  // output column blocks
+  constexpr int SR = 32 * TN;               // slab rows
+  static_assert(!GEGLU || TN % 2 == 0, "GEGLU needs value and gate blocks");
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lg = lane >> 5;
+  const int t = xcd_tile(blockIdx.x, gridDim.x);
+  const int nt = t / chunks, mc = t - nt * chunks;
+  const int n0 = nt * 32 * TNO;
+  const int KB = K >> 6, S = K >> 4;  // 64-wide k blocks, k16 steps
+  const int row = (mc * 4 + wave) * 32 + l32;  // this lane's output row
+  const int64_t xoff = (int64_t)(row < M ? row : M - 1) * ldx + 8 * lg;
+
+  uint4v xf[P];
+#pragma unroll
+  for (int p = 0; p < P; p++) xf[p] = *(const uint4v*)(X + xoff + 16 * p);
+  // epilogue inputs: the residual and the bias of the lane's 4-column groups
+  // (8-byte loads where aligned: R rows are, ldr % 8 == 0; the bias may be a
+  // view at any offset, and its gate half starts at N)
+  const bool bvec = bias != nullptr && ((uintptr_t)bias & 7) == 0 && (!GEGLU || (N & 3) == 0);
+  uint2v rres[TNO][4], rb[TNO][4], rbg[TNO][4];
+#pragma unroll
+  for (int j = 0; j < TNO; j++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int col = n0 + 32 * j + 8 * g + 4 * lg;
+      const bool whole = row < M && col + 4 <= N;
+      rres[j][g] = R != nullptr && whole ? *(const uint2v*)(R + (int64_t)row * ldr + col) : uint2v{0, 0};
+      rb[j][g] = bvec && col + 4 <= N ? *(const uint2v*)(bias + col) : uint2v{0, 0};
+      rbg[j][g] = GEGLU && bvec && col + 4 <= N ? *(const uint2v*)(bias + N + col) : uint2v{0, 0};
+    }
+  // the slab: DMA instruction q (of wave q % 4) fills block q, i.e. slab rows
+  // 8 * (q / KB) + lane / 8, k block q % KB; lane l fetches chunk (l%8) ^ (row%8)
+  const int nq = (SR / 8) * KB;
+  for (int q = wave; q < nq; q += 4) {
+    const int rb8 = q / KB, kb = q - rb8 * KB;
+    const int r = rb8 * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+    const bool gate = GEGLU && r >= SR / 2;
+    const int cc = n0 + (gate ? r - SR / 2 : r);
+    const int wrow = (cc < N ? cc : N - 1) + (gate ? N : 0);  // rows past N: clamped, never stored
+    __builtin_amdgcn_global_load_lds((const void*)(W + (int64_t)wrow * K + kb * 64 + c * 8),
+                                     (__attribute__((address_space(3))) void*)(smem + q * 512), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): everything above has landed
+  __syncthreads();
+  if ((mc * 4 + wave) * 32 >= M) return;  // a wave past the last row (after the barrier: its DMA share is done)
+
+  // W fragment of column block j, k16 step s (slab row 32 j + l32)
+  auto wfrag = [&](int j, int s) __attribute__((always_inline)) -> uint4v {
+    const int r = 32 * j + l32, c = (2 * s + lg) & 7;
+    return *(const uint4v*)(smem + ((r >> 3) * KB + (s >> 2)) * 512 + (r & 7) * 64 + ((c ^ (r & 7)) << 3));
+  };
+  float16v acc[TN];
+#pragma unroll
+  for (int j = 0; j < TN; j++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc[j][e] = 0.f;
+  for (int s0 = 0; s0 < S; s0 += P) {  // S % P == 0
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+      uint4v b[TN];
+#pragma unroll
+      for (int j = 0; j < TN; j++) b[j] = wfrag(j, s0 + p);
+#pragma unroll
+      for (int j = 0; j < TN; j++) acc[j] = mfma32<BF16>(b[j], xf[p], acc[j]);
+      if (s0 + P < S) xf[p] = *(const uint4v*)(X + xoff + 16 * (s0 + P + p));  // K longer than the registers
+    }
+  }
+
+  // bias, one rounding, GeGLU on the lane's (value, gate) pair, the residual,
+  // as the other kernels; lane l holds row l % 32 and columns 8*g + 4*(l/32) +
+  // {0..3} of each column block
+  if (row >= M) return;
+#pragma unroll
+  for (int j = 0; j < TNO; j++) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int col = n0 + 32 * j + 8 * g + 4 * lg;
+      if (col >= N) continue;
+      const bool whole = col + 4 <= N;
+      const uint32_t bw[2] = {rb[j][g].x, rb[j][g].y}, bgw[2] = {rbg[j][g].x, rbg[j][g].y};
+      const uint32_t rw[2] = {rres[j][g].x, rres[j][g].y};
+      uint16_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float bv = 0.f, bg = 0.f;
+        if (bias != nullptr) {
+          if (whole && bvec) {
+            bv = to_f<BF16>((bw[e >> 1] >> (16 * (e & 1))) & 0xffff);
+            if constexpr (GEGLU) bg = to_f<BF16>((bgw[e >> 1] >> (16 * (e & 1))) & 0xffff);
+          } else if (col + e < N) {
+            bv = to_f<BF16>(bias[col + e]);
+            if constexpr (GEGLU) bg = to_f<BF16>(bias[N + col + e]);
+          }
+        }
+        float v = to_f<BF16>(from_f<BF16>(acc[j][4 * g + e] + bv));
+        if constexpr (GEGLU) {
+          const float gt = to_f<BF16>(from_f<BF16>(acc[j + TN / 2][4 * g + e] + bg));
+          v = pin_f32(gelu_fast(v) * gt);  // the f32 product, then one rounding to the storage type
+        }
+        o[e] = from_f<BF16>(v);
+        if (R != nullptr) {
+          const uint16_t r16 = whole ? (uint16_t)((rw[e >> 1] >> (16 * (e & 1))) & 0xffff)
+                                     : (col + e < N ? R[(int64_t)row * ldr + col + e] : (uint16_t)0);
+          o[e] = from_f<BF16>(to_f<BF16>(o[e]) + to_f<BF16>(r16));
+        }
+      }
+      uint16_t* yp = Y + (int64_t)row * ldy + col;
+      if (whole) {
+        *(uint2v*)yp = uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+      } else {
+        for (int e = 0; col + e < N; e++) yp[e] = o[e];
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------ large-M MFMA kernel
@@ -860,6 +1006,41 @@ void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64
                                (pan & HB_Y_PANEL) ? 1 : 0);
 }
 
+// Small-M launcher for 16-bit weights: slabs of 32 (GeGLU: 64) W rows, 128
+// rows of X per block.  P (X steps held in registers) is the largest of 48,
+// 36, 32, 24, 16 and 4 that divides K/16.
+template <int TN, bool BF16, bool GEGLU>
+void launch_slab_t(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias,
+                   const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K) {
+  constexpr int TNO = GEGLU ? TN / 2 : TN;
+  const int tiles_n = (N + 32 * TNO - 1) / (32 * TNO), chunks = (M + 127) / 128;
+  const size_t lds = (size_t)32 * TN * K * sizeof(uint16_t);
+  HB_REQUIRE(lds <= 160 * 1024, "hb_linear: weight slab too large for LDS");
+  const int S = K / 16;
+  auto go = [&](auto kern) {
+    static std::atomic<uint64_t> attr{0};
+    once_per_device(attr, [&] {
+      HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    });
+    kern<<<tiles_n * chunks, 256, lds, st>>>(x, ldx, w, bias, r, ldr, y, ldy, M, N, K, chunks);
+  };
+  if (S % 48 == 0) go(gemm_slab<TN, 48, BF16, GEGLU>);
+  else if (S % 36 == 0) go(gemm_slab<TN, 36, BF16, GEGLU>);
+  else if (S % 32 == 0) go(gemm_slab<TN, 32, BF16, GEGLU>);
+  else if (S % 24 == 0) go(gemm_slab<TN, 24, BF16, GEGLU>);
+  else if (S % 16 == 0) go(gemm_slab<TN, 16, BF16, GEGLU>);
+  else go(gemm_slab<TN, 4, BF16, GEGLU>);
+}
+
+// The slab kernel pays off while its blocks fit one per CU: its X fragment
+// loads (32 rows x 32 bytes each) are bound by the CU's L1 (about 15 bytes
+// per clock for that pattern), so two blocks on one CU take twice as long and
+// the 128 x 128 kernel, which stages X through LDS, is faster from there on.
+inline bool slab_path(int64_t M, int64_t N_out, int64_t K, bool geglu, int cus) {
+  const int64_t tiles_n = (N_out + 31) / 32, chunks = (M + 127) / 128;
+  return K % 64 == 0 && K * 32 * (geglu ? 2 : 1) * 2 <= 160 * 1024 && tiles_n * chunks <= cus;
+}
+
 // The large-M kernel runs for M >= 4096; it is the only one that takes
 // panel-order operands (the entry points check that before dispatching).
 inline bool arow_path(int64_t M) { return M >= 4096; }
@@ -868,13 +1049,21 @@ template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
 void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
                           QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
                           int N, int K) {
-  // large M: persistent 256 x 192 tiles with register-resident A rows; otherwise 128 x 128
+  // large M: persistent 256 x 192 tiles with register-resident A rows; small
+  // M: weight-stationary slabs (16-bit weights), else 128 x 128 tiles
   if (arow_path(M) && K % 64 == 0)
     launch_arow<192, BF16, GEGLU, QB, AFF, SF32, false>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   else if (arow_path(M))
     launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-  else
+  else {
+    if constexpr (QB == 0) {
+      if (slab_path(M, N, K, GEGLU, cus)) {
+        launch_slab_t<GEGLU ? 2 : 1, BF16, GEGLU>(st, x, ldx, w, bias, r, ldr, y, ldy, M, N, K);
+        return;
+      }
+    }
     launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+  }
 }
 
 template <int QB, bool AFF, bool SF32>

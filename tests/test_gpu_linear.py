@@ -246,3 +246,48 @@ def test_small_output_linear_epilogues(b):
     C.dispose_quantized(b, Q)
     for t in (X, Wt, Bt, R, Xq):
         b.dispose(t)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_small_m_slab_edges_and_bits_equal_large_m(b, dtype):
+    """The weight-stationary small-M kernel (16-bit weights, K % 64 == 0) on
+    its edges: rows not a multiple of 32, output widths that end inside a
+    32-column block, a bias that is an offset view (not 8-byte aligned),
+    GeGLU, residuals, K from 64 to 1152.  Against the oracle (max-rel 2e-3 /
+    8e-3), and bit for bit against the large-M kernel: the same X rows placed
+    in a 4096-row input give the same output rows.  (Output rows of a length
+    that is not a multiple of 8 take the f32 SIMT kernels instead, whose
+    summation order depends on the shape.)"""
+    rng = np.random.default_rng(21)
+    cases = [(77, 784, 192, True, "offset", False), (300, 2304, 768, True, "aligned", False),
+             (1, 768, 1152, False, "aligned", True), (129, 200, 1024, False, None, True),
+             (33, 96, 64, False, "offset", True), (500, 2304, 768, False, None, False)]
+    for (M, N2, K, geglu, bmode, resid) in cases:
+        x = rounded(rng.standard_normal((M, K)), dtype)
+        w = rounded(rng.normal(0, 0.05, (N2, K)), dtype)
+        N = N2 // 2 if geglu else N2
+        bias = rounded(rng.standard_normal(N2 + 1), dtype)
+        r = rounded(rng.standard_normal((M, N)), dtype)
+        X, Wt, Bfull, R = (b.fromHost(to_host(a, dtype)) for a in (x, w, bias, r))
+        Bt = None if bmode is None else (b.slice(Bfull, [1], [N2 + 1]) if bmode == "offset" else b.slice(Bfull, [0], [N2]))
+        bv = None if bmode is None else (bias[1:] if bmode == "offset" else bias[:N2])
+        y = b.linear(X, Wt, Bt)
+        y = b.geglu(y) if geglu else y
+        y = b.add(R, y) if resid else y
+        got = read32(b, y)
+        lin = rounded(cr.linear(x, w, bv), dtype)
+        ref = rounded(cr.geglu(lin), dtype) if geglu else lin
+        ref = r + ref if resid else ref
+        err = max_rel(got, ref)
+        assert err <= (2e-3 if dtype == "f16" else 8e-3), f"M={M} N={N2} K={K} geglu={geglu}: {err:.2e}"
+        # the same rows through the large-M kernel
+        xb = np.concatenate([x, rounded(rng.standard_normal((4096 - M, K)), dtype)])
+        rb = np.concatenate([r, rounded(rng.standard_normal((4096 - M, N)), dtype)])
+        XB, RB = b.fromHost(to_host(xb, dtype)), b.fromHost(to_host(rb, dtype))
+        yb = b.linear(XB, Wt, Bt)
+        yb = b.geglu(yb) if geglu else yb
+        yb = b.add(RB, yb) if resid else yb
+        big = np.asarray(b.read(yb).data)
+        np.testing.assert_array_equal(np.asarray(b.read(y).data), big[:M])
+        for t in (X, Wt, Bfull, R, y, XB, RB, yb) + ((Bt,) if Bt is not None else ()):
+            b.dispose(t)
