@@ -40,6 +40,16 @@ __device__ __forceinline__ uint16_t from_f(float v) {
 // LDS element offset of 16-byte chunk c of row r in a [rows][64] u16 tile.
 __device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
 
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane l
+// fills LDS bytes [lds + 16 l, lds + 16 l + 16), `lds` being the wave's
+// (wave-uniform) LDS byte address.  Issued from inline asm, so the compiler
+// neither orders later LDS accesses behind it nor counts it in its own load
+// waits (an extra load in flight only makes those waits stronger); the
+// caller waits for it (vmcnt) before anything reads the destination.
+__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+
 // Tile index for block `bid` of `nb`: contiguous runs of tiles per XCD.
 __device__ __forceinline__ int xcd_tile(int bid, int nb) {
   int xcd = bid & 7, idx = bid >> 3;
@@ -171,7 +181,18 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
   const int m0 = (tile / tiles_n) * BM;
   const int n0 = (tile % tiles_n) * BNO;  // first output column (pair index for GEGLU)
 
-  // B tile row r -> W row (GEGLU: first half value rows, second half gate rows)
+  // B tile row r -> W row (GEGLU: first half value rows, second half gate
+  // rows).  wlane: byte offsets of the lane's W pieces from the tile's first
+  // row of their half; load i holds rows 32i + tid/8, gate rows from
+  // i = B_LD / 2 on.
+  static_assert(!GEGLU || (B_LD % 2 == 0 && (B_LD / 2) * (NT / 8) == BN / 2), "GEGLU halves of the W loads");
+  uint32_t wlane[B_LD];
+#pragma unroll
+  for (int i = 0; i < B_LD; i++) {
+    const int q = tid + i * NT, r = q >> 3, c = q & 7;
+    const int rr = GEGLU && r >= BN / 2 ? r - BN / 2 : r;
+    wlane[i] = (uint32_t)(((int64_t)rr * K + c * 8) * 2);
+  }
   auto w_row = [&](int r) -> int {
     if constexpr (GEGLU) return r < BN / 2 ? n0 + r : N + n0 + (r - BN / 2);
     else return n0 + r;
@@ -585,7 +606,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // Loads are branch-free: addresses are clamped into the operand.  Rows past
   // M (A) or N (W) only feed outputs that are never stored, so they need no
   // zeroing; a K tail (K % 64 != 0, KTAIL, row-major X only) is zeroed.
+  //
+  // Without a K tail the loads are buffer loads: the resource's base is the
+  // first row of the tile (wave-uniform, 64-bit), the lanes' offsets from it
+  // are kernel constants and the K position is the scalar offset, so a stage
+  // spends no vector instructions on addresses.  Rows past the operand lie
+  // outside the resource's range and read 0.
+  constexpr bool BUFX = !KTAIL, BUFW = QB == 0 && !KTAIL;
+  constexpr int BUF_FLAGS = 0x00020000;  // resource word 3: 32-bit raw data
+  uint32_t xlane[TM];                    // byte offsets of the lane's rows in a tile
+#pragma unroll
+  for (int rb = 0; rb < TM; rb++) {
+    const int lr = wave * 64 + rb * 32 + l32;
+    xlane[rb] = (uint32_t)(((lr >> 5) * xs_hi + (lr & 31) * xs_lo + xk * lg * 8) * 2);
+  }
+  const int64_t x_elems = xpan ? (int64_t)mlim * K : (int64_t)(M - 1) * ldx + K;
   auto load_a = [&](int m0, int k0, uint4v (&a)[TM][KS]) {
+    if constexpr (BUFX) {
+      const int64_t base = xpan ? (int64_t)(m0 >> 5) * xs_hi : (int64_t)m0 * ldx;
+      const int64_t left = (x_elems - base) * 2;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(X + base), (short)0, (int)(left < 0x7ffffff0 ? left : 0x7ffffff0), BUF_FLAGS);
+#pragma unroll
+      for (int rb = 0; rb < TM; rb++)
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+          a[rb][s] = __builtin_amdgcn_raw_buffer_load_b128(rs, xlane[rb], (k0 + s * 16) * xk * 2, 0);
+      return;
+    }
     const int arow = m0 + wave * 64 + l32;
 #pragma unroll
     for (int rb = 0; rb < TM; rb++)
@@ -604,8 +652,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     uint32_t s[QB ? B_LD : 1], z[QB ? B_LD : 1];
     float sf[QB && SF32 ? B_LD : 1], zf[QB && SF32 ? B_LD : 1];
   };
-  // B tile row r -> W row (GEGLU: first half value rows, second half gate rows)
+  // B tile row r -> W row (GEGLU: first half value rows, second half gate
+  // rows).  wlane: byte offsets of the lane's W pieces from the tile's first
+  // row of their half; load i holds rows 32i + tid/8, gate rows from
+  // i = B_LD / 2 on.
+  static_assert(!GEGLU || (B_LD % 2 == 0 && (B_LD / 2) * (NT / 8) == BN / 2), "GEGLU halves of the W loads");
+  uint32_t wlane[B_LD];
+#pragma unroll
+  for (int i = 0; i < B_LD; i++) {
+    const int q = tid + i * NT, r = q >> 3, c = q & 7;
+    const int rr = GEGLU && r >= BN / 2 ? r - BN / 2 : r;
+    wlane[i] = (uint32_t)(((int64_t)rr * K + c * 8) * 2);
+  }
   auto load_b = [&](int n0, int k0, BRegs& br) {
+    if constexpr (BUFW) {
+      // value rows from W row n0, gate rows (GEGLU) from W row N + n0; each
+      // resource ends with row N - 1 of its half
+      const int64_t left = ((int64_t)(N - n0) * K) * 2;
+      const int nrec = (int)(left < 0x7ffffff0 ? left : 0x7ffffff0);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(W + (int64_t)n0 * K), (short)0, nrec, BUF_FLAGS);
+      const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(W + (int64_t)((GEGLU ? N : 0) + n0) * K), (short)0, nrec, BUF_FLAGS);
+#pragma unroll
+      for (int i = 0; i < B_LD; i++)
+        br.v[i] = __builtin_amdgcn_raw_buffer_load_b128(GEGLU && i >= B_LD / 2 ? rg : rv, wlane[i], k0 * 2, 0);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < B_LD; i++) {
       const int q = tid + i * NT, r = q >> 3, c = q & 7;
@@ -679,18 +752,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // writes its own slot, so slots outside the operand load a clamped,
   // in-bounds address (ldr % 8 == 0: a chunk starting below N lies inside the
   // row) and are never stored.
+  // The copies are issued from inline asm (lds_copy16): the compiler then
+  // does not take the fragment reads and W stores of the following stages for
+  // possible readers of the C tile, each of which it would otherwise precede
+  // with a wait for every load in flight.  The epilogue waits for them.
   auto dma_resid = [&](int m0, int n0) {
     int ln = lane, wv = wave;
     asm volatile("" : "+v"(ln), "+v"(wv));  // per-tile address math, not hoisted (see the epilogue)
     const int r_cx = (ln & 7) ^ (ln >> 3);
     const int rbase = m0 + wv * 8 + (ln >> 3), cbase = n0 + r_cx * 8;
+    const uint32_t cs0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)Cs +
+                         (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 1024u;
 #pragma unroll
     for (int i = 0; i < RG * 8; i++) {
       const int row = rbase + (i & 7) * 32, col = cbase + (i >> 3) * 64;
       const bool cok = (i >> 3) * 8 + r_cx < CPR && col < N;
-      __builtin_amdgcn_global_load_lds((const void*)(R + (int64_t)(row < M ? row : M - 1) * ldr + (cok ? col : 0)),
-                                       (__attribute__((address_space(3))) void*)(Cs + (i * 4 + wv) * 512), 16, 0,
-                                       0);
+      lds_copy16(R + (int64_t)(row < M ? row : M - 1) * ldr + (cok ? col : 0), cs0 + (uint32_t)i * 4096u);
     }
   };
 
@@ -809,63 +886,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   };
 
-  // Spread write-out: in a block that streams several tiles, an interior
-  // tile's output waits in the C tile and leaves during the first
-  // WO_STAGES stages of the next tile (PER_STAGE 16-byte chunks per thread
-  // and stage) instead of in one burst that every CU issues at the same
-  // moment.  The residual DMA of the next tile then starts at stage
-  // res_stage, after the C tile has drained.
-  constexpr int WO_STAGES = 6, PER_STAGE = BM * CPR / NT / WO_STAGES;
-  static_assert(PER_STAGE * WO_STAGES * NT == BM * CPR, "write-out parts");
-  const bool spread = KT >= 2 * WO_STAGES;
-  const int res_stage = spread ? WO_STAGES : 0;
-  int wo_m0 = -1, wo_n0 = 0, it_cur = 0;  // wo_m0 < 0: no output pending
-  // part `part` (0..WO_STAGES-1) of the pending output; the values are
-  // computed in every tile's first stages (branch-free, between the MFMAs)
-  // and stored only when an output is pending (the block's first tile has
-  // none: its C tile then holds nothing of use)
-  auto write_part = [&](int part) __attribute__((always_inline)) {
-    int t0 = tid;
-    asm volatile("" : "+v"(t0));
-    uint4v v[PER_STAGE];
-    int64_t off[PER_STAGE];
-#pragma unroll
-    for (int k = 0; k < PER_STAGE; k++) {
-      const int q = t0 + (part * PER_STAGE + k) * NT;
-      int r, c;
-      if (ypan) {
-        off[k] = panel_chunk(q, r, c);
-      } else {
-        r = q / CPR;
-        c = q - r * CPR;
-        off[k] = (int64_t)r * ldy + c * 8;
-      }
-      v[k] = out_chunk(r, c);
-    }
-    if (wo_m0 >= 0) {
-      uint16_t* yb = ypan ? Y + ((int64_t)(wo_m0 >> 5) * yblk + (wo_n0 >> 4)) * 512 : Y + (int64_t)wo_m0 * ldy + wo_n0;
-#pragma unroll
-      for (int k = 0; k < PER_STAGE; k++) *(uint4v*)(yb + off[k]) = v[k];
-    }
-  };
-
   uint4v A0[TM][KS], A1[TM][KS], A2[TM][KS];
   BRegs B0, B1;
   // step g: MFMAs on `ac` and LDS buffer g&1; loads stage g+2 of the stream
   // into (al, bl); stages the W tile of g+1 (held in bs) into the other buffer.
-  // WP: this stage also writes part `kin` of the previous tile's output
-  // (branch-free inside the stage, so the scheduler can put its LDS reads,
-  // VALU work and stores between the MFMAs)
-  auto step = [&](auto wp, int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl,
+  //
+  // Origins of the block's current tile and of the tile after it, set per
+  // tile, so that a stage finds the tile of the stage it loads with scalar
+  // selects (for the last tile nxt = cur, nxt_kb = (KT - 1) * BK and
+  // nxt_ks = 0: loads past the end of the stream repeat its last stage).
+  int cur_m0 = 0, cur_n0 = 0, nxt_m0 = 0, nxt_n0 = 0, nxt_kb = 0, nxt_ks = 0;
+  auto step = [&](int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl,
                   BRegs& bs) __attribute__((always_inline)) {
-    constexpr bool WP = decltype(wp)::value;
-    // the residual tile arrives while the tile computes, once the previous
-    // tile's output has left the C tile (at once for a block's first tile)
-    if (R != nullptr && kin == (it_cur == 0 ? 0 : res_stage)) dma_resid(tile_m0(it_cur), tile_n0(it_cur));
-    const int g2 = g + 2 < S ? g + 2 : S - 1;
-    const int i2 = g2 / KT, k2 = (g2 - i2 * KT) * BK;
-    load_a(tile_m0(i2), k2, al);
-    load_b(tile_n0(i2), k2, bl);
+    // the residual tile arrives in the C tile while the tile computes (the
+    // previous tile's output has left it)
+    if (R != nullptr && kin == 0) dma_resid(cur_m0, cur_n0);
+    // stage g + 2 of the stream: stage kin + 2 of this tile, or stage
+    // kin + 2 - KT of the next (a block with several tiles has KT >= 6)
+    const int k2 = __builtin_amdgcn_readfirstlane(kin + 2);
+    const int wrap = __builtin_amdgcn_readfirstlane(k2 >= KT ? 1 : 0);
+    const int m2 = __builtin_amdgcn_readfirstlane(wrap ? nxt_m0 : cur_m0);
+    const int n2 = __builtin_amdgcn_readfirstlane(wrap ? nxt_n0 : cur_n0);
+    const int k2b = __builtin_amdgcn_readfirstlane(wrap ? nxt_kb + (k2 - KT) * nxt_ks : k2 * BK);
+    load_a(m2, k2b, al);
+    load_b(n2, k2b, bl);
     const uint16_t* b = Bs + (g & 1) * BN * BK;
     uint4v bf[KS][TN];
 #pragma unroll
@@ -878,19 +922,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int j = 0; j < TN; j++)
 #pragma unroll
         for (int i = 0; i < TM; i++) acc[i][j] = mfma32<BF16>(bf[s][j], ac[i][s], acc[i][j]);
-    if constexpr (WP) write_part(kin);
     // schedule: substep-0 fragment reads, then MFMA pairs, each preceded by
     // one global load (while any remain) and one fragment read of the next
-    // substep (and, writing out, a share of the VALU work); the W staging for
-    // the next stage goes last
+    // substep; the W staging for the next stage goes last
     constexpr int NVMEM = TM * KS + B_LD, NPAIR = KS * TN;
-    constexpr int NVALU = WP ? 1 : 0;
     __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
 #pragma unroll
     for (int p = 0; p < NPAIR; p++) {
       if (p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       if (p < (KS - 1) * TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (NVALU) __builtin_amdgcn_sched_group_barrier(0x002, NVALU, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
     }
     store_b((g + 1) & 1, bs);
@@ -912,32 +952,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // only when KT % 6 == 0 (the launcher gives every block one tile otherwise).
   for (int it = 0; it < ntile; it++) {
     const int g0 = it * KT;
-    it_cur = it;
-    // six stages (the register rotation's period); with WP, stages 0..5 of
-    // the tile, each writing a sixth of the previous tile's output
-    auto six = [&](auto wp, int kt) __attribute__((always_inline)) {
-      step(wp, g0 + kt, kt, A0, A2, B0, B1);
-      if (kt + 1 < KT) step(wp, g0 + kt + 1, kt + 1, A1, A0, B1, B0);
-      if (kt + 2 < KT) step(wp, g0 + kt + 2, kt + 2, A2, A1, B0, B1);
-      if (kt + 3 < KT) step(wp, g0 + kt + 3, kt + 3, A0, A2, B1, B0);
-      if (kt + 4 < KT) step(wp, g0 + kt + 4, kt + 4, A1, A0, B0, B1);
-      if (kt + 5 < KT) step(wp, g0 + kt + 5, kt + 5, A2, A1, B1, B0);
-    };
-    six(std::true_type{}, 0);  // stages 0..5 write the previous tile's output, if pending
-    wo_m0 = -1;
-    for (int kt = 6; kt < KT; kt += 6) six(std::false_type{}, kt);
-    // the residual DMA (stage res_stage < KT - 1) has landed once at most the
-    // W and A loads of one stage are outstanding (they were all issued after
-    // it, and loads complete in order); the barrier makes every wave's part
-    // of the C tile visible (and, without R, keeps the previous tile's
-    // write-out reads ahead of this epilogue's writes)
+    cur_m0 = tile_m0(it);
+    cur_n0 = tile_n0(it);
+    const bool has_next = it + 1 < ntile;
+    nxt_m0 = has_next ? tile_m0(it + 1) : cur_m0;
+    nxt_n0 = has_next ? tile_n0(it + 1) : cur_n0;
+    nxt_kb = has_next ? 0 : (KT - 1) * BK;
+    nxt_ks = has_next ? BK : 0;
+    // six stages at a time (the register rotation's period)
+    for (int kt = 0; kt < KT; kt += 6) {
+      step(g0 + kt, kt, A0, A2, B0, B1);
+      if (kt + 1 < KT) step(g0 + kt + 1, kt + 1, A1, A0, B1, B0);
+      if (kt + 2 < KT) step(g0 + kt + 2, kt + 2, A2, A1, B0, B1);
+      if (kt + 3 < KT) step(g0 + kt + 3, kt + 3, A0, A2, B1, B0);
+      if (kt + 4 < KT) step(g0 + kt + 4, kt + 4, A1, A0, B0, B1);
+      if (kt + 5 < KT) step(g0 + kt + 5, kt + 5, A2, A1, B1, B0);
+    }
+    // the residual DMA (issued at stage 0, before that stage's loads) has
+    // landed once at most the W and A loads of one stage are outstanding
+    // (they were all issued after it, and loads complete in order); the
+    // barrier makes every wave's part of the C tile visible (and, without R,
+    // keeps the previous tile's write-out reads ahead of this epilogue's
+    // writes)
     static_assert(TM * KS + B_LD <= 15, "vmcnt immediate");
     if (R != nullptr) __builtin_amdgcn_s_waitcnt(0x0F70 | (TM * KS + B_LD));
     __syncthreads();
     {
       using T = std::true_type;
       using F = std::false_type;
-      const int n0 = tile_n0(it);
+      const int n0 = cur_n0;
       if (bias == nullptr) {
         if (R == nullptr) epilogue(n0, F{}, F{});
         else epilogue(n0, F{}, T{});
@@ -953,14 +996,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
     __syncthreads();
-    const int m0 = tile_m0(it), n0 = tile_n0(it);
-    if (spread && it + 1 < ntile && m0 + BM <= M && n0 + BNO <= N) {
-      wo_m0 = m0;  // leaves during the next tile's first stages
-      wo_n0 = n0;
-    } else {
-      write_out(m0, n0);
-      if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
-    }
+    write_out(cur_m0, cur_n0);
+    if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
   }
 }
 
