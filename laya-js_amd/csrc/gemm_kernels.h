@@ -959,14 +959,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     nxt_n0 = has_next ? tile_n0(it + 1) : cur_n0;
     nxt_kb = has_next ? 0 : (KT - 1) * BK;
     nxt_ks = has_next ? BK : 0;
-    // six stages at a time (the register rotation's period)
-    for (int kt = 0; kt < KT; kt += 6) {
+    // Six stages at a time (the register rotation's period), with no branch
+    // between them: the compiler places its load waits by tracking which
+    // registers have loads in flight, and where paths that ran different
+    // numbers of stages join it must assume the union of their loads, which
+    // makes a stage wait for the loads issued one stage earlier (for the
+    // stage after next) and halves the latency the stream hides.
+    int kt = 0;
+    for (; kt + 6 <= KT; kt += 6) {
+      step(g0 + kt, kt, A0, A2, B0, B1);
+      step(g0 + kt + 1, kt + 1, A1, A0, B1, B0);
+      step(g0 + kt + 2, kt + 2, A2, A1, B0, B1);
+      step(g0 + kt + 3, kt + 3, A0, A2, B1, B0);
+      step(g0 + kt + 4, kt + 4, A1, A0, B0, B1);
+      step(g0 + kt + 5, kt + 5, A2, A1, B1, B0);
+    }
+    // The last KT % 6 stages: blocks with one tile only (the launcher
+    // streams several tiles per block only when KT % 6 == 0).  Every load
+    // is drained after them, so the join after this tail leaves the
+    // compiler's view of the loads in flight exactly that of the loop above.
+    if (kt < KT) {
       step(g0 + kt, kt, A0, A2, B0, B1);
       if (kt + 1 < KT) step(g0 + kt + 1, kt + 1, A1, A0, B1, B0);
       if (kt + 2 < KT) step(g0 + kt + 2, kt + 2, A2, A1, B0, B1);
       if (kt + 3 < KT) step(g0 + kt + 3, kt + 3, A0, A2, B1, B0);
       if (kt + 4 < KT) step(g0 + kt + 4, kt + 4, A1, A0, B0, B1);
-      if (kt + 5 < KT) step(g0 + kt + 5, kt + 5, A2, A1, B1, B0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     // the residual DMA (issued at stage 0, before that stage's loads) has
     // landed once at most the W and A loads of one stage are outstanding
