@@ -87,8 +87,9 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_mfma_arow_config3_hbm_cou
 
 def _is_dominant(key: str) -> bool:
     """linear[M=..,N=..,K=..] launches served by the large-M f16 kernel with a
-    plain (non-GeGLU) epilogue."""
-    return key.startswith("linear[") and "geglu" not in key and int(key.split("M=")[1].split(",")[0]) >= 4096
+    plain epilogue (not GeGLU, not the fused q / k / v projection)."""
+    return (key.startswith("linear[") and "geglu" not in key and ",qkv" not in key
+            and int(key.split("M=")[1].split(",")[0]) >= 4096)
 
 
 def _key_flops(key: str) -> float:
@@ -134,7 +135,7 @@ def run_encode(args) -> dict:
     cfg = parseModernBertConfig(BASE)
     W = make_weights(BASE)
 
-    be = HipBackend(0)
+    be = HipBackend(0, fuse_qkv=args.fuse_qkv)
     info = be.device_info()
     log(f"device: {info}")
     t0 = time.time()
@@ -178,7 +179,7 @@ def run_encode(args) -> dict:
 
     # second timed region: HIP events around every linear launch (on the
     # backend's stream) -> per-launch GPU time by shape
-    be.startProfiling(only={"hb_linear"})
+    be.startProfiling(only={"hb_linear", "hb_linear_qkv"})
     gpu_ms2, _, _ = timed(args.steps)
     prof = be.stopProfiling()
     log(f"instrumented region: {gpu_ms2 / args.steps:.3f} ms/step")
@@ -255,7 +256,7 @@ def run_encode(args) -> dict:
         "config": {
             "workload": "BASELINE config 3: ModernBERT-base-shape encoder forward, B=32, T=512, 22 layers, "
                         "hidden 768, 12 heads, GeGLU 1152, local window 128 / global every 3rd layer",
-            "global_batch": B, "seq_len": T, "parallelism": "single GPU",
+            "global_batch": B, "seq_len": T, "parallelism": "single GPU", "fuse_qkv": bool(args.fuse_qkv),
             "padded_tokens_per_step": tokens, "valid_tokens_per_step": valid_tokens,
             "valid_tokens_per_s": valid_tokens / (ms_per_step * 1e-3),
             "linear_tflop_per_step": lin_flops / 1e12,
@@ -549,6 +550,9 @@ def main():
     ap.add_argument("--mode", choices=["encode", "gemm", "copy", "config0", "config4"], default="encode")
     ap.add_argument("--copy-mib", type=int, default=512, help="buffer size for --mode copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--fuse-qkv", action="store_true",
+                    help="encode with HipBackend(fuse_qkv=True): the q / k / v projection written head-major with "
+                         "RoPE in its epilogue (hb_linear_qkv)")
     ap.add_argument("--cpu-sample", type=int, default=8, help="sequences in the CPU-baseline sample")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -188,6 +188,22 @@ int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintptr_t w, uint
  *  also needs N % 16 == 0 and no residual.  Other calls fail.  The
  *  arithmetic is the same as with row-major operands, bit for bit. */
 
+/* The attention block's q / k / v projection fused with its layout glue
+ * and RoPE: y = x . w^T for the stacked projection w [3*H*64, K] (no bias,
+ * as ModernBERT's attention_bias = false; `bias` must be 0),
+ * written head-major as y[3][B][H][L][64] (B = M / L, rows of x ordered
+ * b * L + t), with the split-half rotation of base `rope_base` applied to the
+ * q and k parts (none when rope_base <= 0), each value rounded to dt after
+ * the product and again after the rotation -- bit for bit what
+ * Backend.linear (tensor-backend/src/index.ts:211-215), reshape / transpose /
+ * split (index.ts:169-176) and Backend.rope (index.ts:225-229) store when
+ * called as modernbert/src/index.ts:348-351 does.
+ *  dt     HB_F16 / HB_BF16 (x, w, y).
+ *  Needs M >= 4096, K % 64 == 0, M % L == 0, 16-byte aligned operands;
+ *  flags: HB_X_PANEL (x in panel order) only. */
+int hb_linear_qkv(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintptr_t w, uintptr_t bias, uintptr_t y,
+                  int64_t M, int64_t K, int64_t L, int64_t H, double rope_base, unsigned flags);
+
 /* Quantized linear: y = x . dequant(W)^T (+ epilogue), W [N, K] in the
  * laya-js quantized layout v1 (HostQuantized, tensor-backend/src/index.ts:98-115;
  * docs/QUANTIZATION.md "Format"): `qw` row-major packed bytes, K*bits/8 per

@@ -35,6 +35,8 @@
 
 namespace hb {
 
+const float* rope_table(uintptr_t ctx, int64_t L, int64_t D, double base);
+
 // ------------------------------------------------------------------ SIMT kernel (f32 path, fallback)
 
 struct QWs {  // quantized weight for the SIMT kernel (bits = 0: plain)
@@ -218,6 +220,32 @@ extern "C" int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintpt
     }
   }
   check_launch("hb_linear");
+  HB_API_END
+}
+
+extern "C" int hb_linear_qkv(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintptr_t w, uintptr_t bias,
+                             uintptr_t y, int64_t M, int64_t K, int64_t L, int64_t H, double rope_base,
+                             unsigned flags) {
+  HB_API_BEGIN
+  HB_REQUIRE(dt == HB_F16 || dt == HB_BF16, "hb_linear_qkv: dtype must be f16 or bf16");
+  HB_REQUIRE(arow_path(M) && M < (1ll << 31) && K > 0 && K % 64 == 0 && K < (1ll << 30),
+             "hb_linear_qkv: needs M >= 4096 and K % 64 == 0");
+  HB_REQUIRE(L > 0 && M % L == 0 && H > 0 && H < (1 << 20), "hb_linear_qkv: M must be a multiple of L, H > 0");
+  HB_REQUIRE((flags & ~(unsigned)HB_X_PANEL) == 0 && bias == 0,
+             "hb_linear_qkv: takes no bias and no flag but HB_X_PANEL");
+  HB_REQUIRE(x % 16 == 0 && w % 16 == 0 && y % 16 == 0 && ((flags & HB_X_PANEL) || (ldx >= K && ldx % 8 == 0)),
+             "hb_linear_qkv: operands must be 16-byte aligned (ldx % 8 == 0)");
+  const float2* tab = rope_base > 0 ? (const float2*)rope_table(ctx, L, 64, rope_base) : nullptr;
+  const QK qk{tab, (int)L, (int)H};
+  const unsigned pan = flags & HB_X_PANEL;
+  const int N = (int)(3 * H * 64);
+  if (dt == HB_F16)
+    launch_qkv<false>(stream_of(ctx), cu_count(ctx), pan, (const uint16_t*)x, ldx, (const uint16_t*)w, (uint16_t*)y,
+                      (int)M, N, (int)K, qk);
+  else
+    launch_qkv<true>(stream_of(ctx), cu_count(ctx), pan, (const uint16_t*)x, ldx, (const uint16_t*)w, (uint16_t*)y,
+                     (int)M, N, (int)K, qk);
+  check_launch("hb_linear_qkv");
   HB_API_END
 }
 

@@ -8,4 +8,9 @@ template void mfma_dtype<0, false, false>(int, bool, hipStream_t, int, unsigned,
                                           const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
                                           uint16_t*, int64_t, int, int, int);
 
+template void launch_qkv<false>(hipStream_t, int, unsigned, const uint16_t*, int64_t, const uint16_t*, uint16_t*, int,
+                                int, int, QK);
+template void launch_qkv<true>(hipStream_t, int, unsigned, const uint16_t*, int64_t, const uint16_t*, uint16_t*, int,
+                               int, int, QK);
+
 }  // namespace hb

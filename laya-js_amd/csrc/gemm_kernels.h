@@ -115,6 +115,15 @@ struct QW {  // quantized weight operand
   int group;  // values per group
 };
 
+// The fused-projection epilogue (QKV): y = x . W^T with W the
+// stacked [3 * H * 64, K] q / k / v projection, written head-major as
+// [3][B][H][L][64] (B = M / L) with RoPE applied to the q and k parts.
+struct QK {
+  const float2* tab;  // RoPE cos / sin [L][32], or null: no rotation
+  int L;              // sequence length (M = B * L)
+  int H;              // heads (N = 3 * H * 64)
+};
+
 // Copies a [BM][BNO] 16-bit tile staged in LDS to Y with 16-byte coalesced
 // stores; with a residual, y = round(tile + resid) (linear, then add).
 template <bool BF16, int BM, int BNO, int NT>
@@ -555,11 +564,18 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
 // as the B operand): lane l then holds output row l % 32 and the four
 // consecutive columns 8*(r/4) + 4*(l/32) + {0..3} of each accumulator, so the
 // epilogue writes 8-byte pieces of Y straight from registers.
-template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
+//
+// QKV (16-bit weights, no GeGLU, no bias, no residual): the epilogue of the fused
+// q / k / v projection (struct QK): each 64-column head of the tile is a pair
+// of column blocks whose lanes hold the rotation partners d and d + 32 at the
+// same register, so RoPE is applied in registers, and the tile leaves
+// head-major.
+template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL, bool QKV = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_mfma_arow(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W, QW qw,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
-    int64_t ldy, int M, int N, int K, int tiles_n, int tiles, int xpan, int ypan) {
+    int64_t ldy, int M, int N, int K, int tiles_n, int tiles, int xpan, int ypan, QK qk) {
+  static_assert(!QKV || (!GEGLU && QB == 0 && BN % 64 == 0), "QKV: 16-bit weights, whole heads per tile");
   constexpr int NT = 256, BM = 256, BK = 64;
   constexpr int TM = 2, TN = BN / 32;  // 32x32 blocks per wave
   constexpr int KS = BK / 16;          // k16 substeps per stage
@@ -886,6 +902,87 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   };
 
+  // ---- QKV epilogue: one rounding to the storage type (the linear
+  // output), then, for a head of q or k, the split-half rotation of that
+  // rounded value in f32 and a second rounding (a separate Backend.rope),
+  // into the C tile.  Head pair hp of the tile is column blocks 2hp (dims
+  // 0..31) and 2hp + 1 (dims 32..63); a lane holds dims 8g + 4lg + e of both.
+  auto epilogue_qkv = [&](int m0, int n0) {
+    int l32 = lane & 31, lg = lane >> 5, wv = wave;
+    asm volatile("" : "+v"(l32), "+v"(lg), "+v"(wv));
+    // the QK fields are re-read here (through an empty asm), so what is
+    // derived from them is computed per tile, not held across the K loop
+    int L = qk.L, H = qk.H;
+    const float2* tab = qk.tab;
+    asm volatile("" : "+s"(L), "+s"(H), "+s"(tab));
+    const int HD = H * 64;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int row = wv * 64 + i * 32 + l32;
+      const int pos = (m0 + row < M ? m0 + row : M - 1) % L;
+      // cos / sin of dims 8g + 4lg + 0..3 at this row's position
+      float4v cs[4][2];
+      if (tab != nullptr && n0 < 2 * HD) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4v* t = (const float4v*)(tab + (int64_t)pos * 32 + 8 * g + 4 * lg);
+          cs[g][0] = t[0];
+          cs[g][1] = t[1];
+        }
+      }
+#pragma unroll
+      for (int hp = 0; hp < TN / 2; hp++) {
+        const int c0 = 64 * hp;                                   // tile column of the head's dim 0
+        const bool rot = tab != nullptr && n0 + c0 < 2 * HD;     // a head of q or k
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int col = c0 + 8 * g + 4 * lg;  // tile column of dim 8g + 4lg
+          uint16_t o0[4], o1[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            o0[e] = from_f<BF16>(acc[i][2 * hp][4 * g + e]);
+            o1[e] = from_f<BF16>(acc[i][2 * hp + 1][4 * g + e]);
+          }
+          if (rot) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const float c = cs[g][e >> 1][2 * (e & 1)], sn = cs[g][e >> 1][2 * (e & 1) + 1];
+              const float x0 = to_f<BF16>(o0[e]), x1 = to_f<BF16>(o1[e]);
+              o0[e] = from_f<BF16>(pin_f32(fmaf(-x1, sn, x0 * c)));
+              o1[e] = from_f<BF16>(pin_f32(fmaf(x0, sn, x1 * c)));
+            }
+          }
+          *(uint2v*)(Cs + r_slot(row, col >> 3) * 8 + (col & 7)) =
+              uint2v{(uint32_t)o0[0] | ((uint32_t)o0[1] << 16), (uint32_t)o0[2] | ((uint32_t)o0[3] << 16)};
+          *(uint2v*)(Cs + r_slot(row, (col + 32) >> 3) * 8 + (col & 7)) =
+              uint2v{(uint32_t)o1[0] | ((uint32_t)o1[1] << 16), (uint32_t)o1[2] | ((uint32_t)o1[3] << 16)};
+        }
+      }
+    }
+  };
+  // ---- QKV write-out: 8 threads per tile row, thread t8 takes the 16-byte
+  // chunk t8 of each head (dims 8 t8 .. 8 t8 + 7), so 8 threads write one
+  // head row of 128 bytes and a wave 8 consecutive rows of one head
+  auto write_out_qkv = [&](int m0, int n0) {
+    int t0 = tid, L = qk.L, H = qk.H;
+    asm volatile("" : "+v"(t0), "+s"(L), "+s"(H));
+    const int t8 = t0 & 7, HD = H * 64, Bn = M / L;
+#pragma unroll 1
+    for (int r = t0 >> 3; r < BM; r += NT / 8) {
+      const int gm = m0 + r;
+      if (gm >= M) break;
+      const int bb = gm / L, tt = gm - bb * L;
+#pragma unroll
+      for (int hp = 0; hp < BNO / 64; hp++) {
+        const int gn = n0 + 64 * hp;  // the head's first column
+        if (gn >= N) break;
+        const int part = gn / HD, hh = (gn - part * HD) >> 6;
+        uint16_t* dst = Y + ((((int64_t)part * Bn + bb) * H + hh) * L + tt) * 64 + 8 * t8;
+        *(uint4v*)dst = out_chunk(r, 8 * hp + t8);
+      }
+    }
+  };
+
   uint4v A0[TM][KS], A1[TM][KS], A2[TM][KS];
   BRegs B0, B1;
   // step g: MFMAs on `ac` and LDS buffer g&1; loads stage g+2 of the stream
@@ -999,7 +1096,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       using T = std::true_type;
       using F = std::false_type;
       const int n0 = cur_n0;
-      if (bias == nullptr) {
+      if constexpr (QKV) {
+        epilogue_qkv(cur_m0, n0);
+      } else if (bias == nullptr) {
         if (R == nullptr) epilogue(n0, F{}, F{});
         else epilogue(n0, F{}, T{});
       } else {
@@ -1014,7 +1113,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
     __syncthreads();
-    write_out(cur_m0, cur_n0);
+    if constexpr (QKV) write_out_qkv(cur_m0, cur_n0);
+    else write_out(cur_m0, cur_n0);
     if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
   }
 }
@@ -1038,10 +1138,10 @@ void launch_mfma(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t*
   kern<<<tiles_m * tiles_n, WM * WN * 64, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n);
 }
 
-template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL>
+template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL, bool QKV = false>
 void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
                         QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
-                        int N, int K) {
+                        int N, int K, QK qk = QK{nullptr, 1, 1}) {
   constexpr int BNO = GEGLU ? BN / 2 : BN;
   const int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO, tiles = tiles_m * tiles_n;
   // one persistent block per CU, a multiple of 8 (one per XCD); with
@@ -1052,13 +1152,13 @@ void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64
   HB_REQUIRE(grid >= 8, "hb_linear: large-M GEMM needs at least 8 tiles");
   constexpr int RG = (BNO / 8 + 7) / 8;
   const size_t lds = ((size_t)2 * BN * 64 + (size_t)RG * 256 * 64) * sizeof(uint16_t);
-  auto kern = gemm_mfma_arow<BN, BF16, GEGLU, QB, AFF, SF32, KTAIL>;
+  auto kern = gemm_mfma_arow<BN, BF16, GEGLU, QB, AFF, SF32, KTAIL, QKV>;
   static std::atomic<uint64_t> attr{0};
   once_per_device(attr, [&] {
     HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   });
   kern<<<grid, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n, tiles, (pan & HB_X_PANEL) ? 1 : 0,
-                               (pan & HB_Y_PANEL) ? 1 : 0);
+                               (pan & HB_Y_PANEL) ? 1 : 0, qk);
 }
 
 // Small-M launcher for 16-bit weights: slabs of 32 (GeGLU: 64) W rows, 128
@@ -1134,7 +1234,20 @@ void mfma_dtype(int dt, bool geglu, hipStream_t st, int cus, unsigned pan, const
   }
 }
 
+// The fused q / k / v projection (16-bit weights, M >= 4096, K % 64 == 0):
+// the large-M kernel with the QKV epilogue.
+template <bool BF16>
+void launch_qkv(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                uint16_t* y, int M, int N, int K, QK qk) {
+  launch_arow<192, BF16, false, 0, false, false, false, true>(st, cus, pan, x, ldx, w, QW{}, nullptr, nullptr, 0, y,
+                                                              0, M, N, K, qk);
+}
+
 // Instantiated by gemm_f16.hip (QB = 0), gemm_q8.hip and gemm_q4.hip.
+extern template void launch_qkv<false>(hipStream_t, int, unsigned, const uint16_t*, int64_t, const uint16_t*,
+                                       uint16_t*, int, int, int, QK);
+extern template void launch_qkv<true>(hipStream_t, int, unsigned, const uint16_t*, int64_t, const uint16_t*,
+                                      uint16_t*, int, int, int, QK);
 extern template void mfma_dtype<0, false, false>(int, bool, hipStream_t, int, unsigned, const uint16_t*, int64_t,
                                                  const uint16_t*, QW, const uint16_t*, const uint16_t*, int64_t,
                                                  uint16_t*, int64_t, int, int, int);

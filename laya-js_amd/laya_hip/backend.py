@@ -295,17 +295,96 @@ class _PendingLinear:
 
 
 class _PendingRope:
+    """rope not yet launched (index.ts:225-229): applied by sdpa while it
+    stages q / k, or by hb_linear_qkv when x is a view of the pending q / k / v
+    projection (`lin`, a _SharedLinear; src's storage is None until that
+    product is launched row-major)."""
+
     def __init__(self, be, x, base):
         self.be = be
         self.x = x
         self.base = float(base)
-        self.ref = x._st.retain()
+        self.lin = x._lazy.share() if isinstance(x._lazy, _SharedLinear) else None
+        self.ref = x._st.retain() if self.lin is None else None
         self.src = (x._st, x._off, x._strides, x.dtype, x.shape)
+
+    def source(self):
+        """(storage, offset, strides, dtype, shape) of the unrotated input,
+        launching a pending product row-major first."""
+        if self.lin is not None and self.src[0] is None:
+            st = self.lin.rowmajor()
+            self.ref = st.retain()
+            self.src = (st,) + self.src[1:]
+        return self.src
 
     def release(self):
         if self.ref is not None:
             self.ref.release()
             self.ref = None
+        if self.lin is not None:
+            self.lin.release()
+            self.lin = None
+
+
+class _SharedLinear:
+    """A pending plain linear whose result has only been viewed so far
+    (reshape / transpose / slice keep their strides over the [M, N] output).
+    The views share this object; the first reader launches the product
+    row-major (`rowmajor`).  sdpa on roped q / k views and the v view of the
+    stacked q / k / v projection, laid out as ModernBert.layer takes them
+    (modernbert/src/index.ts:348-351), instead launches hb_linear_qkv once
+    (`fused`): the product written head-major with the q and k heads rotated,
+    the values a separate linear, transpose / split and rope would store."""
+
+    def __init__(self, be, lin: "_PendingLinear", M: int, N: int, dtype: str):
+        self.be, self.lin, self.M, self.N, self.dtype = be, lin, M, N, dtype
+        self.users = 1
+        self.st = None       # the row-major output, once launched
+        self.fused_st = {}   # (rope base, L, H) -> storage of the head-major [3, B, H, L, 64] output
+
+    def share(self) -> "_SharedLinear":
+        self.users += 1
+        return self
+
+    def release(self):
+        self.users -= 1
+        if self.users == 0:
+            self.lin.release()
+            if self.st is not None:
+                self.st.release()
+                self.st = None
+            for st in self.fused_st.values():
+                st.release()
+            self.fused_st = {}
+
+    def rowmajor(self):
+        if self.st is None:
+            be = self.be
+            self.st = be._malloc(self.M * self.N * DT[self.dtype][1])
+            be.stats["linear"] += 1
+            self.lin.launch(self.st.ptr, self.N)
+        return self.st
+
+    def qkv_ok(self) -> bool:
+        """hb_linear_qkv's conditions on the product itself."""
+        lin = self.lin
+        return (lin.epi == 0 and lin.q is None and lin.bp == 0 and lin.arow_ok and self.dtype in ("f16", "bf16")
+                and self.N % 192 == 0 and lin.x[2] % 64 == 0 and lin.wp % 16 == 0)
+
+    def fused(self, base: float, L: int, H: int):
+        key = (float(base), L, H)
+        st = self.fused_st.get(key)
+        if st is None:
+            be, lin = self.be, self.lin
+            xp, M, K, ldx = lin.x
+            st = be._malloc(M * self.N * DT[self.dtype][1])
+            flags = F.HB_X_PANEL if lin.panel is not None else 0
+            be.stats["linear"] += 1
+            be.stats["linear_fused_qkv"] += 1
+            be._call("linear", "hb_linear_qkv", be.ctx, DT[self.dtype][0], xp, ldx, lin.wp, 0, st.ptr, M, K, L,
+                     H, float(base), flags)
+            self.fused_st[key] = st
+        return st
 
 
 class _PendingSdpa:
@@ -406,7 +485,13 @@ class HipBackend:
 
     name = "hip"
 
-    def __init__(self, device: int = 0, lib_path: str | None = None):
+    def __init__(self, device: int = 0, lib_path: str | None = None, fuse_qkv: bool = False):
+        """`fuse_qkv`: launch an attention block's q / k / v projection as
+        hb_linear_qkv (the product written head-major with RoPE applied in the
+        GEMM's epilogue) when sdpa consumes it as ModernBert.layer does.  Off
+        by default: on the ModernBERT-base shape it is slower than rotating q
+        and k while sdpa stages them."""
+        self.fuse_qkv = bool(fuse_qkv)
         self.n = F.native(lib_path)
         ctx = F.U(0)
         self.n.call("createHipBackend", "hb_init", device, F.C.byref(ctx))
@@ -419,12 +504,12 @@ class HipBackend:
         self._blocks: dict[int, list[int]] = {}
         self._capture_held: Optional[list] = None  # blocks disposed while a capture records
         self._capture_summaries: Optional[set] = None  # summaries already enqueued into the recording
-        self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "sdpa": 0,
+        self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "linear_fused_qkv": 0, "sdpa": 0,
                       "sdpa_fused_rope": 0, "copies": 0, "panel_unpacks": 0}
 
     # ---------------------------------------------------------------- plumbing
     # kernel-launching entry points (timed per op key while profiling)
-    _LAUNCHES = frozenset(("hb_linear", "hb_qlinear", "hb_qgather", "hb_layernorm", "hb_layernorm_panel",
+    _LAUNCHES = frozenset(("hb_linear", "hb_linear_qkv", "hb_qlinear", "hb_qgather", "hb_layernorm", "hb_layernorm_panel",
                            "hb_panel_unpack", "hb_panel_pack", "hb_rope", "hb_sdpa", "hb_sdpa_mask_info", "hb_geglu",
                            "hb_unary", "hb_binary", "hb_where", "hb_gather", "hb_reduce", "hb_scan", "hb_meanpool"))
 
@@ -436,7 +521,9 @@ class HipBackend:
             self.n.call(op, name, *args)
             self.n.call(op, "hb_event_record", self.ctx, b)
             key = op
-            if name in ("hb_linear", "hb_qlinear"):
+            if name == "hb_linear_qkv":
+                key = f"{op}[M={args[7]},N={3 * 64 * args[10]},K={args[8]},qkv]"
+            elif name in ("hb_linear", "hb_qlinear"):
                 key = f"{op}[M={args[10]},N={args[11]},K={args[12]}{',geglu' if args[-1] & F.HB_EPI_GEGLU else ''}]" \
                     if name == "hb_linear" else f"{op}[M={args[12]},N={args[13]},K={args[14]},q{args[15]}]"
             prof.append((key, a, b))
@@ -569,6 +656,9 @@ class HipBackend:
         elif isinstance(lz, _PendingSdpa):
             t._st = lz.rowmajor().retain()  # t keeps its view (offset, strides) of the [B, Lq, H, D] output
             lz.release()
+        elif isinstance(lz, _SharedLinear):
+            t._st = lz.rowmajor().retain()  # t keeps its view (offset, strides) of the [M, N] output
+            lz.release()
         elif isinstance(lz, _PanelRows):
             st = self._malloc(_numel(t.shape) * DT[t.dtype][1])
             t._st, t._off, t._strides = st, 0, _contig(t.shape)
@@ -582,7 +672,7 @@ class HipBackend:
                 self._call("read", "hb_panel_unpack", self.ctx, lz.st.ptr, st.ptr, lz.K, lz.M, lz.K)
             lz.release()
         elif isinstance(lz, _PendingRope):
-            src_st, off, strides, dtype, shape = lz.src
+            src_st, off, strides, dtype, shape = lz.source()
             st = self._malloc(_numel(t.shape) * DT[t.dtype][1])
             t._st, t._off, t._strides = st, 0, _contig(t.shape)
             B, H, L, D = self._bhld(shape)
@@ -861,6 +951,15 @@ class HipBackend:
         return {"live_bytes": a.value, "cached_bytes": b.value, "live_blocks": c.value}
 
     # ---------------------------------------------------------------- shape
+    def _shared_linear(self, x: HipTensor) -> Optional[_SharedLinear]:
+        """x's pending plain product as a _SharedLinear that views may share
+        (x itself becomes the first view), or None."""
+        lz = x._lazy
+        if isinstance(lz, _PendingLinear) and lz.epi == 0 and x._off == 0 and len(x.shape) >= 1:
+            x._lazy = _SharedLinear(self, lz, _numel(x.shape[:-1]), lz.n_out, x.dtype)
+            x._strides = _contig(x.shape)
+        return x._lazy if isinstance(x._lazy, _SharedLinear) else None
+
     def reshape(self, x: HipTensor, shape) -> HipTensor:
         self._live(x, op="reshape")
         shape = [int(d) for d in shape]
@@ -872,7 +971,8 @@ class HipBackend:
             shape[shape.index(-1)] = n // known if known else 0
         if _numel(shape) != n:
             raise ValueError(f"reshape: cannot reshape [{','.join(map(str, x.shape))}] to [{','.join(map(str, shape))}]")
-        if isinstance(x._lazy, _PendingSdpa):  # a view of the pending output, not launched yet
+        if isinstance(x._lazy, _PendingSdpa) or self._shared_linear(x) is not None:
+            # a view of the pending output, not launched yet
             st = self._nocopy_strides(x.shape, x._strides, shape)
             if st is not None:
                 return self._track(HipTensor(shape, x.dtype, None, x._off, st, lazy=x._lazy.share()))
@@ -941,7 +1041,8 @@ class HipBackend:
         perm = [int(p) % len(x.shape) if len(x.shape) else 0 for p in perm]
         if sorted(perm) != list(range(len(x.shape))):
             raise ValueError(f"transpose: bad perm {perm} for rank {len(x.shape)}")
-        if isinstance(x._lazy, _PendingSdpa):  # a view of the pending output, not launched yet
+        if isinstance(x._lazy, _PendingSdpa) or self._shared_linear(x) is not None:
+            # a view of the pending output, not launched yet
             return self._track(HipTensor([x.shape[p] for p in perm], x.dtype, None, x._off,
                                          [x._strides[p] for p in perm], lazy=x._lazy.share()))
         self._ready(x)
@@ -949,7 +1050,9 @@ class HipBackend:
 
     def slice(self, x: HipTensor, begin, end) -> HipTensor:
         self._live(x, op="slice")
-        self._ready(x)
+        lazy_view = self._shared_linear(x) is not None  # a view of a pending product stays pending
+        if not lazy_view:
+            self._ready(x)
         r = len(x.shape)
         if len(begin) > r or len(end) > r:
             raise ValueError("slice: more bounds than axes")
@@ -967,6 +1070,8 @@ class HipBackend:
             e = min(max(e, b), n)
             off += b * x._strides[i]
             shape[i] = e - b
+        if lazy_view:
+            return self._track(HipTensor(shape, x.dtype, None, off, x._strides, lazy=x._lazy.share()))
         return self._view(x, shape, x._strides, off)
 
     def split(self, x: HipTensor, parts: int, axis: int) -> list:
@@ -1353,7 +1458,8 @@ class HipBackend:
         self._live(x, op="rope")
         if x.shape[-1] % 2:
             raise ValueError("rope: head dim must be even")
-        self._ready(x)
+        if not isinstance(x._lazy, _SharedLinear):  # a view of a pending product stays pending
+            self._ready(x)
         dt = x.dtype if x.dtype in FLOAT_DT else "f32"
         if self._bhld_strides(x.shape, x._strides) is None:
             x = self._contiguous(x)
@@ -1364,7 +1470,7 @@ class HipBackend:
         """(ptr, strides[4], rope_base, storage) of a [B, H, L, D] sdpa operand."""
         lz = t._lazy
         if isinstance(lz, _PendingRope) and lz.src[3] == t.dtype:
-            st, off, strides, dtype, shape = lz.src
+            st, off, strides, dtype, shape = lz.source()
             return st.ptr + off * DT[dtype][1], self._bhld_strides(shape, strides), lz.base, st
         self._ready(t)
         s = self._bhld_strides(t.shape, t._strides)
@@ -1372,6 +1478,31 @@ class HipBackend:
             t = self._contiguous(t)
             s = self._bhld_strides(t.shape, t._strides)
         return self._ptr(t), s, 0.0, t._st
+
+    def _qkv_fused(self, q: HipTensor, k: HipTensor, v: HipTensor):
+        """sdpa operands from one hb_linear_qkv launch, when q and k are
+        roped views and v a view of the same pending [B*L, 3*H*64] projection,
+        taken as modernbert/src/index.ts:348-351 takes them (reshape to
+        [B, L, 3, H, 64], transpose to [3, B, H, L, 64], split); else None."""
+        lq, lk, S = q._lazy, k._lazy, v._lazy
+        if not (self.fuse_qkv and isinstance(lq, _PendingRope) and isinstance(lk, _PendingRope) and isinstance(S, _SharedLinear)):
+            return None
+        if lq.lin is not S or lk.lin is not S or lq.base != lk.base or lq.base <= 0 or not S.qkv_ok():
+            return None
+        B, H, L, D = q.shape
+        if D != 64 or tuple(k.shape) != tuple(q.shape) or tuple(v.shape) != tuple(q.shape) or B * L != S.M \
+                or S.N != 3 * H * 64 or not (q.dtype == k.dtype == v.dtype == S.dtype):
+            return None
+        rows = (L * S.N, 64, S.N, 1)  # [B, H, L, 64] over the [B*L, 3*H*64] product
+        for (_, off, strides, dtype, shape), want in ((lq.src, 0), (lk.src, H * 64)):
+            if off != want or tuple(strides) != rows or tuple(shape) != tuple(q.shape) or dtype != S.dtype:
+                return None
+        if v._off != 2 * H * 64 or tuple(v._strides) != rows:
+            return None
+        st = S.fused(lq.base, L, H)
+        part = B * H * L * 64 * DT[S.dtype][1]
+        hs = (H * L * 64, L * 64, 64, 1)
+        return [(st.ptr + i * part, hs, 0.0, st) for i in range(3)]
 
     def sdpa(self, q: HipTensor, k: HipTensor, v: HipTensor, mask: Optional[HipTensor], scale: float) -> HipTensor:
         self._live(q, k, v, mask, op="sdpa")
@@ -1384,11 +1515,13 @@ class HipBackend:
         dt = _promote(_promote(q.dtype, k.dtype), v.dtype)
         if dt not in FLOAT_DT:
             dt = "f32"
-        ops = []
-        for t in (q, k, v):
-            if t.dtype != dt:
-                t = self.cast(t, dt)
-            ops.append(self._attn_operand(t))
+        ops = self._qkv_fused(q, k, v)
+        if ops is None:
+            ops = []
+            for t in (q, k, v):
+                if t.dtype != dt:
+                    t = self.cast(t, dt)
+                ops.append(self._attn_operand(t))
         (qp, qs, rq, qst), (kp, ks, rk, kst), (vp, vs, _, vst) = ops
         refs = [qst.retain(), kst.retain(), vst.retain()]
         mp, ms = 0, None
@@ -1576,6 +1709,6 @@ class HipBackend:
         return ms.value
 
 
-def createHipBackend(device: int = 0, lib_path: str | None = None) -> HipBackend:
+def createHipBackend(device: int = 0, lib_path: str | None = None, fuse_qkv: bool = False) -> HipBackend:
     """Factory named like the reference's createMlxBackend / createWebGpuBackend."""
-    return HipBackend(device, lib_path)
+    return HipBackend(device, lib_path, fuse_qkv)

@@ -57,6 +57,7 @@ SYMBOLS: dict[str, tuple] = {
     "hb_graph_launch": (I, [U, U]),
     "hb_graph_destroy": (I, [U, U]),
     "hb_linear": (I, [U, I, U, I64, U, U, U, I64, U, I64, I64, I64, I64, C.c_uint]),
+    "hb_linear_qkv": (I, [U, I, U, I64, U, U, U, I64, I64, I64, I64, D, C.c_uint]),
     "hb_qlinear": (I, [U, I, U, I64, U, U, U, U, U, I64, U, I64, I64, I64, I64, I, I, I, C.c_uint]),
     "hb_qgather": (I, [U, U, U, U, I64, I64, I, I, I, U, I64, I, U]),
     "hb_layernorm": (I, [U, I, U, I64, I, U, U, I, U, I64, I64, F]),
