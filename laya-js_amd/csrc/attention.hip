@@ -155,6 +155,24 @@ __device__ __forceinline__ uint32_t mask_bits(uint32_t w) {
   return ((nz >> 7) * 0x01020408u) >> 24;
 }
 
+// Cross-lane exchanges for the 4 lanes that hold one query (lane, lane ^ 16,
+// lane ^ 32, lane ^ 48): ds_swizzle in bit-mask mode (and 0x1f, xor 0x10)
+// reads lane ^ 16 within each half-wave; v_permlane32_swap exchanges the
+// two halves, returning (per lane) its own value and the one of lane ^ 32.
+__device__ __forceinline__ float from_xor16(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
 __device__ __forceinline__ int qk_swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
 // K tiles: chunk c of row r at c ^ (4 * bit 1 of r + bits 3..4 of r).  A
 // 16-lane pass of the S = K.Q^T fragment reads touches rows b + 8a (a, b in
@@ -387,12 +405,13 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
     l[qb] = 0.f;
   }
 
-  // online softmax of one 64-key tile for query block qb: scores sv (raw,
-  // -inf where hidden) -> P fragments, running max / sum, O rescale
+  // online softmax of one 64-key tile for query block qb: scores st (raw,
+  // -inf where hidden; lane key 32t + 8g + e is st[2t + e/4][e%4]) -> P
+  // fragments, running max / sum, O rescale
   uint4v pf[kQB][2];
-  auto softmax = [&](int qb, float (&sv)[2][8], float mx) {
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  auto softmax = [&](int qb, const float4v (&sq)[4], float mx) {
+    mx = fmaxf(mx, from_xor16(mx));
+    mx = max_xor32(mx);
     const float mnew = fmaxf(m[qb], mx);  // raw (unscaled) row max
     const float mc = mnew == -INFINITY ? 0.f : mnew * scale_log2;
     const float alpha = __builtin_amdgcn_exp2f(m[qb] * scale_log2 - mc);
@@ -403,8 +422,8 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
       uint32_t pk[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[t][e], scale_log2, -mc));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[t][e + 1], scale_log2, -mc));
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sq[2 * t + (e >> 2)][e & 3], scale_log2, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sq[2 * t + (e >> 2)][(e & 3) + 1], scale_log2, -mc));
         psum += p0 + p1;
         pk[e >> 1] = pack2<BF16>(p0, p1);
       }
@@ -453,43 +472,30 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
       if (mask != nullptr && wave_class(nk) == 2) load_mask(nk, mwn);
     }
 
-    // ---- mask (only for mixed tiles), online softmax, P fragments
-    if (cl == 0) {
-    } else if (cl == 1) {
+    // ---- mask (only for mixed tiles, in place), online softmax, P fragments
+    if (cl != 0) {
 #pragma unroll
       for (int qb = 0; qb < kQB; qb++) {
-        float sv[2][8];
-        float mx = -INFINITY;
+        if (cl == 2) {
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+          for (int t = 0; t < 2; t++) {
+            const int kbase = k0 + 32 * t + 8 * g;  // this lane's 8 contiguous keys
+            // bit e of vis: key kbase + e is visible (mask byte nonzero, key < Lk)
+            uint32_t vis = 0xffu;
+            if (mask != nullptr) vis = mask_bits(mw[qb][t].x) | (mask_bits(mw[qb][t].y) << 4);
+            const int left = Lk - kbase;
+            if (left < 8) vis &= left > 0 ? (1u << left) - 1u : 0u;
 #pragma unroll
-          for (int e = 0; e < 8; e++) {
-            sv[t][e] = e < 4 ? st[qb][2 * t][e] : st[qb][2 * t + 1][e - 4];
-            mx = fmaxf(mx, sv[t][e]);
-          }
-        softmax(qb, sv, mx);
-      }
-    } else {
-#pragma unroll
-      for (int qb = 0; qb < kQB; qb++) {
-        float sv[2][8];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-          const int kbase = k0 + 32 * t + 8 * g;  // this lane's 8 contiguous keys
-          // bit e of vis: key kbase + e is visible (mask byte nonzero, key < Lk)
-          uint32_t vis = 0xffu;
-          if (mask != nullptr) vis = mask_bits(mw[qb][t].x) | (mask_bits(mw[qb][t].y) << 4);
-          const int left = Lk - kbase;
-          if (left < 8) vis &= left > 0 ? (1u << left) - 1u : 0u;
-#pragma unroll
-          for (int e = 0; e < 8; e++) {
-            const float sc = e < 4 ? st[qb][2 * t][e] : st[qb][2 * t + 1][e - 4];
-            sv[t][e] = (vis >> e) & 1u ? sc : -INFINITY;
-            mx = fmaxf(mx, sv[t][e]);
+            for (int e = 0; e < 8; e++)
+              st[qb][2 * t + (e >> 2)][e & 3] = (vis >> e) & 1u ? st[qb][2 * t + (e >> 2)][e & 3] : -INFINITY;
           }
         }
-        softmax(qb, sv, mx);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) mx = fmaxf(mx, st[qb][kb][e]);
+        softmax(qb, st[qb], mx);
       }
     }
 
@@ -519,8 +525,8 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
 #pragma unroll
   for (int qb = 0; qb < kQB; qb++) {
     float lt = l[qb];
-    lt += __shfl_xor(lt, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
+    lt += from_xor16(lt);
+    lt = sum_xor32(lt);
     const float inv = 1.0f / lt;
     const int q = q0 + wave * 16 * kQB + qb * 16 + li;
     if (q >= Lq) continue;

@@ -879,11 +879,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       return;
     }
     if (m0 + BM <= M && n0 + BNO <= N) {  // interior tile: no bounds checks
-      uint16_t* yb = Y + (int64_t)m0 * ldy + n0;
+      // TPR threads per row, chunks c = t % TPR + TPR * j: a pass covers
+      // NT / TPR rows (a multiple of 8, so a thread's C-tile slots differ
+      // only by the pass: immediate LDS offsets), and every address is a
+      // per-thread row pointer plus constants.  Two passes' LDS reads are
+      // issued before their stores.
+      constexpr int TPR = CPR % 8 == 0 ? 8 : 4, CPT = CPR / TPR, RPP = NT / TPR, NP = BM / RPP;
+      static_assert(CPR % TPR == 0 && RPP % 8 == 0 && NP % 2 == 0, "interior write-out layout");
+      const int tc = t0 % TPR, tr = t0 / TPR;
+      uint16_t* yr = Y + (int64_t)(m0 + tr) * ldy + n0 + tc * 8;
+      const int64_t ystep = (int64_t)RPP * ldy;
 #pragma unroll
-      for (int k = 0; k < BM * CPR / NT; k++) {
-        const int q = t0 + k * NT, r = q / CPR, c = q - r * CPR;
-        *(uint4v*)(yb + (int64_t)r * ldy + c * 8) = out_chunk(r, c);
+      for (int p = 0; p < NP; p += 2) {
+        uint4v v[2][CPT];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+          for (int j = 0; j < CPT; j++) v[h][j] = out_chunk(tr + (p + h) * RPP, tc + TPR * j);
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+          for (int j = 0; j < CPT; j++) *(uint4v*)(yr + h * ystep + TPR * 8 * j) = v[h][j];
+        yr += 2 * ystep;
       }
       return;
     }
