@@ -772,7 +772,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // does not take the fragment reads and W stores of the following stages for
   // possible readers of the C tile, each of which it would otherwise precede
   // with a wait for every load in flight.  The epilogue waits for them.
-  auto dma_resid = [&](int m0, int n0) {
+  //
+  // They go out in six pieces (DMA_P instructions each), piece p at the end
+  // of stage dma0 + p, after that stage's wait for its W tile.  The compiler
+  // does not count them, so the first load wait issued after a piece also
+  // waits for the piece: one stage later it has landed, whereas copies issued
+  // at the start of a stage would hold that stage's own wait for the whole
+  // residual tile.
+  constexpr int DMA_N = RG * 8, DMA_P = (DMA_N + 5) / 6;
+  auto dma_piece = [&](int m0, int n0, auto P_) __attribute__((always_inline)) {
+    constexpr int P = decltype(P_)::value;
     int ln = lane, wv = wave;
     asm volatile("" : "+v"(ln), "+v"(wv));  // per-tile address math, not hoisted (see the epilogue)
     const int r_cx = (ln & 7) ^ (ln >> 3);
@@ -780,7 +789,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const uint32_t cs0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)Cs +
                          (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 1024u;
 #pragma unroll
-    for (int i = 0; i < RG * 8; i++) {
+    for (int i = P * DMA_P; i < (P + 1) * DMA_P && i < DMA_N; i++) {
       const int row = rbase + (i & 7) * 32, col = cbase + (i >> 3) * 64;
       const bool cok = (i >> 3) * 8 + r_cx < CPR && col < N;
       lds_copy16(R + (int64_t)(row < M ? row : M - 1) * ldr + (cok ? col : 0), cs0 + (uint32_t)i * 4096u);
@@ -919,6 +928,81 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   };
 
+  // ---- spread write-out.  With several tiles per block, an interior tile
+  // leaves the C tile during the next tile's first six stages instead of in
+  // one burst: stage s stores chunks WO_PS * s .. WO_PS * s + WO_PS - 1 of
+  // each thread's WO_N, as buffer stores issued after the stage's loads.
+  // The wait counter counts loads and stores in issue order, so after a
+  // burst the next tile's first load wait also waits for every store of the
+  // tile, which all CUs issue at once; spread, a stage's stores are younger
+  // than every load waited for until two stages later.  Those six stages are
+  // a copy of the stage code of their own (the other stages carry no store
+  // instructions); the resource's record count bounds every store to the
+  // tile.
+  //
+  // Thread t's chunk q: row-major Y as in the interior burst below (WTPR
+  // threads per row, chunk t % WTPR + WTPR * (q % WCPT) of row
+  // t / WTPR + WRPP * (q / WCPT)); panel-order Y chunk t + NT q as in
+  // panel_chunk, whose row block and block column are wave-uniform (lane
+  // offset 16 * lane, scalar block offset).
+  constexpr int WO_N = BM * CPR / NT, WO_PS = WO_N / 6;
+  static_assert(QKV || WO_N % 6 == 0, "spread write-out: whole chunks per stage");
+  constexpr int WTPR = CPR % 8 == 0 ? 8 : 4, WCPT = CPR / WTPR, WRPP = NT / WTPR;
+  // The layout is a compile-time one, panel order for GeGLU (whose output
+  // feeds the next linear) and row-major otherwise; an output in the other
+  // layout leaves in a burst.
+  constexpr bool YP = GEGLU;
+  const bool spread = !QKV && ntile > 1 && KT >= 12 && (ypan != 0) == YP;
+  // the pending output: its first element (row-major) or block (panel
+  // order), and the bytes up to its last chunk (0: nothing pending)
+  uint16_t* wo_base = Y;
+  int wo_rec = 0;
+  // Every address below is recomputed per stage from values re-read through
+  // an empty asm: hoisted out of the stage loop, the addresses of the
+  // chunks would each hold a register for the whole kernel.
+  auto wo_part = [&](auto S_) __attribute__((always_inline)) {
+    constexpr int S = decltype(S_)::value;
+    int t0 = tid, wv = __builtin_amdgcn_readfirstlane(wave), ld2 = (int)ldy * 2, yb = yblk;
+    asm volatile("" : "+v"(t0), "+s"(wv), "+s"(ld2), "+s"(yb));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)wo_base, (short)0, wo_rec, BUF_FLAGS);
+    if constexpr (YP) {
+      // chunk t + NT q: row block rb, block column nb of the tile (scalars)
+      const int ln = t0 & 63, r32 = ln & 31, lx = (ln >> 5) ^ (r32 & 7);
+#pragma unroll
+      for (int u = 0; u < WO_PS; u++) {
+        const int rest = wv + (NT / 64) * (S * WO_PS + u);
+        const int rb = rest / (CPR / 2), nb = rest - rb * (CPR / 2);
+        const int slot = (nb >> 2) * (BM * 8) + (rb * 32 + r32) * 8 + (((nb & 3) * 2) ^ lx);
+        const uint4v v = *(const uint4v*)(Cs + slot * 8);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, ln * 16, (rb * yb + nb) * 1024, 0);
+      }
+    } else {
+      // tile row wtr + WRPP pass, chunk wtc + WTPR j
+      const int wtc = t0 % WTPR, wtr = t0 / WTPR;
+      const int voff = (wtr * ld2) + wtc * 16;
+#pragma unroll
+      for (int u = 0; u < WO_PS; u++) {
+        const int q = S * WO_PS + u, pass = q / WCPT, j = q % WCPT;
+        const int cr = wtc + WTPR * j;
+        const int slot = (cr >> 3) * (BM * 8) + (wtr + WRPP * pass) * 8 + ((cr & 7) ^ (wtr & 7));
+        const uint4v v = *(const uint4v*)(Cs + slot * 8);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, voff, WRPP * pass * ld2 + WTPR * 16 * j, 0);
+      }
+    }
+  };
+  // sets the pending output to tile (m0, n0)
+  auto wo_set = [&](int m0, int n0) {
+    int64_t bytes;
+    if constexpr (YP) {
+      wo_base = Y + ((int64_t)(m0 >> 5) * yblk + (n0 >> 4)) * 512;
+      bytes = ((int64_t)(BM / 32 - 1) * yblk + CPR / 2) * 1024;
+    } else {
+      wo_base = Y + (int64_t)m0 * ldy + n0;
+      bytes = ((int64_t)(BM - 1) * ldy + BNO) * 2;
+    }
+    wo_rec = (int)(bytes < 0x7ffffff0 ? bytes : 0x7ffffff0);
+  };
+
   // ---- QKV epilogue: one rounding to the storage type (the linear
   // output), then, for a head of q or k, the split-half rotation of that
   // rounded value in f32 and a second rounding (a separate Backend.rope),
@@ -1010,11 +1094,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // selects (for the last tile nxt = cur, nxt_kb = (KT - 1) * BK and
   // nxt_ks = 0: loads past the end of the stream repeat its last stage).
   int cur_m0 = 0, cur_n0 = 0, nxt_m0 = 0, nxt_n0 = 0, nxt_kb = 0, nxt_ks = 0;
-  auto step = [&](int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl,
+  // The residual's pieces go out from stage dma0 on, once the C tile is free
+  // (with a spread write-out pending it is read until stage 5), one per
+  // stage up to stage dma0 + dpl, which sends the rest: the last piece then
+  // has one more stage to land before the epilogue, if the tile has it.
+  const int dma0 = spread ? 6 : 0;
+  const int dpl = KT - 2 - dma0 < 0 ? 0 : (KT - 2 - dma0 < 5 ? KT - 2 - dma0 : 5);
+  // S_: the stage's place in its group of six (a compile-time constant)
+  // WO_: whether the stage stores its share of a pending write-out
+  auto step = [&](auto S_, auto WO_, int g, int kin, uint4v (&ac)[TM][KS], uint4v (&al)[TM][KS], BRegs& bl,
                   BRegs& bs) __attribute__((always_inline)) {
-    // the residual tile arrives in the C tile while the tile computes (the
-    // previous tile's output has left it)
-    if (R != nullptr && kin == 0) dma_resid(cur_m0, cur_n0);
+    constexpr int SP = decltype(S_)::value;
+    constexpr bool WO = decltype(WO_)::value && !QKV;
     // stage g + 2 of the stream: stage kin + 2 of this tile, or stage
     // kin + 2 - KT of the next (a block with several tiles has KT >= 6)
     const int k2 = __builtin_amdgcn_readfirstlane(kin + 2);
@@ -1036,19 +1127,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int j = 0; j < TN; j++)
 #pragma unroll
         for (int i = 0; i < TM; i++) acc[i][j] = mfma32<BF16>(bf[s][j], ac[i][s], acc[i][j]);
+    if constexpr (WO) wo_part(S_);
     // schedule: substep-0 fragment reads, then MFMA pairs, each preceded by
     // one global load (while any remain) and one fragment read of the next
-    // substep; the W staging for the next stage goes last
-    constexpr int NVMEM = TM * KS + B_LD, NPAIR = KS * TN;
+    // substep; the write-out's C-tile reads ride with the last loads, its
+    // stores follow every load; the W staging for the next stage goes last
+    constexpr int NVMEM = TM * KS + B_LD, NPAIR = KS * TN, WOS = WO ? WO_PS : 0;
+    static_assert(NVMEM + 2 + WOS <= NPAIR, "write-out stores after the loads");
     __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
 #pragma unroll
     for (int p = 0; p < NPAIR; p++) {
       if (p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       if (p < (KS - 1) * TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (p >= NVMEM - WOS && p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (p >= NVMEM + 2 && p < NVMEM + 2 + WOS) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
     }
     store_b((g + 1) & 1, bs);
     __builtin_amdgcn_sched_group_barrier(0x200, B_LD, 0);
+    // the residual tile arrives in the C tile while the tile computes: piece
+    // p at stage dma0 + min(p, dpl), the last ones together
+    if (R != nullptr && kin - SP == dma0 && SP <= dpl) {
+      dma_piece(cur_m0, cur_n0, S_);
+      if (SP == dpl) {
+        if constexpr (SP < 1) dma_piece(cur_m0, cur_n0, std::integral_constant<int, 1>{});
+        if constexpr (SP < 2) dma_piece(cur_m0, cur_n0, std::integral_constant<int, 2>{});
+        if constexpr (SP < 3) dma_piece(cur_m0, cur_n0, std::integral_constant<int, 3>{});
+        if constexpr (SP < 4) dma_piece(cur_m0, cur_n0, std::integral_constant<int, 4>{});
+        if constexpr (SP < 5) dma_piece(cur_m0, cur_n0, std::integral_constant<int, 5>{});
+      }
+    }
     __syncthreads();
   };
 
@@ -1079,39 +1187,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // numbers of stages join it must assume the union of their loads, which
     // makes a stage wait for the loads issued one stage earlier (for the
     // stage after next) and halves the latency the stream hides.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using I5 = std::integral_constant<int, 5>;
+    using T = std::true_type;
+    using F = std::false_type;
     int kt = 0;
+    // a pending write-out leaves in the tile's first six stages (KT >= 12):
+    // their own copy of the stage code, so that the other stages carry no
+    // store instructions
+    if (wo_rec != 0) {
+      step(I0{}, T{}, g0, 0, A0, A2, B0, B1);
+      step(I1{}, T{}, g0 + 1, 1, A1, A0, B1, B0);
+      step(I2{}, T{}, g0 + 2, 2, A2, A1, B0, B1);
+      step(I3{}, T{}, g0 + 3, 3, A0, A2, B1, B0);
+      step(I4{}, T{}, g0 + 4, 4, A1, A0, B0, B1);
+      step(I5{}, T{}, g0 + 5, 5, A2, A1, B1, B0);
+      wo_rec = 0;
+      kt = 6;
+    }
     for (; kt + 6 <= KT; kt += 6) {
-      step(g0 + kt, kt, A0, A2, B0, B1);
-      step(g0 + kt + 1, kt + 1, A1, A0, B1, B0);
-      step(g0 + kt + 2, kt + 2, A2, A1, B0, B1);
-      step(g0 + kt + 3, kt + 3, A0, A2, B1, B0);
-      step(g0 + kt + 4, kt + 4, A1, A0, B0, B1);
-      step(g0 + kt + 5, kt + 5, A2, A1, B1, B0);
+      step(I0{}, F{}, g0 + kt, kt, A0, A2, B0, B1);
+      step(I1{}, F{}, g0 + kt + 1, kt + 1, A1, A0, B1, B0);
+      step(I2{}, F{}, g0 + kt + 2, kt + 2, A2, A1, B0, B1);
+      step(I3{}, F{}, g0 + kt + 3, kt + 3, A0, A2, B1, B0);
+      step(I4{}, F{}, g0 + kt + 4, kt + 4, A1, A0, B0, B1);
+      step(I5{}, F{}, g0 + kt + 5, kt + 5, A2, A1, B1, B0);
     }
     // The last KT % 6 stages: blocks with one tile only (the launcher
     // streams several tiles per block only when KT % 6 == 0).  Every load
     // is drained after them, so the join after this tail leaves the
     // compiler's view of the loads in flight exactly that of the loop above.
     if (kt < KT) {
-      step(g0 + kt, kt, A0, A2, B0, B1);
-      if (kt + 1 < KT) step(g0 + kt + 1, kt + 1, A1, A0, B1, B0);
-      if (kt + 2 < KT) step(g0 + kt + 2, kt + 2, A2, A1, B0, B1);
-      if (kt + 3 < KT) step(g0 + kt + 3, kt + 3, A0, A2, B1, B0);
-      if (kt + 4 < KT) step(g0 + kt + 4, kt + 4, A1, A0, B0, B1);
+      step(I0{}, F{}, g0 + kt, kt, A0, A2, B0, B1);
+      if (kt + 1 < KT) step(I1{}, F{}, g0 + kt + 1, kt + 1, A1, A0, B1, B0);
+      if (kt + 2 < KT) step(I2{}, F{}, g0 + kt + 2, kt + 2, A2, A1, B0, B1);
+      if (kt + 3 < KT) step(I3{}, F{}, g0 + kt + 3, kt + 3, A0, A2, B1, B0);
+      if (kt + 4 < KT) step(I4{}, F{}, g0 + kt + 4, kt + 4, A1, A0, B0, B1);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
-    // the residual DMA (issued at stage 0, before that stage's loads) has
-    // landed once at most the W and A loads of one stage are outstanding
-    // (they were all issued after it, and loads complete in order); the
+    // The residual's last pieces went out at the end of stage dma0 + dpl, and
+    // memory operations complete in issue order: they have landed once at
+    // most the loads and stores of one later stage are outstanding (or none,
+    // when they went out with the last stage).  The
     // barrier makes every wave's part of the C tile visible (and, without R,
     // keeps the previous tile's write-out reads ahead of this epilogue's
-    // writes)
-    static_assert(TM * KS + B_LD <= 15, "vmcnt immediate");
-    if (R != nullptr) __builtin_amdgcn_s_waitcnt(0x0F70 | (TM * KS + B_LD));
+    // writes).
+    constexpr int VM1 = TM * KS + B_LD;  // the loads of one stage (stages after the pieces store nothing)
+    static_assert(VM1 <= 15, "vmcnt immediate");
+    if (R != nullptr) {
+      if (dma0 + dpl >= KT - 1) __builtin_amdgcn_s_waitcnt(0x0F70);
+      else __builtin_amdgcn_s_waitcnt(0x0F70 | VM1);
+    }
     __syncthreads();
     {
-      using T = std::true_type;
-      using F = std::false_type;
       const int n0 = cur_n0;
       if constexpr (QKV) {
         epilogue_qkv(cur_m0, n0);
@@ -1130,9 +1262,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
     __syncthreads();
-    if constexpr (QKV) write_out_qkv(cur_m0, cur_n0);
-    else write_out(cur_m0, cur_n0);
-    if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
+    if constexpr (QKV) {
+      write_out_qkv(cur_m0, cur_n0);
+    } else if (spread && has_next && cur_m0 + BM <= M && cur_n0 + BNO <= N) {
+      wo_set(cur_m0, cur_n0);  // leaves during the next tile's first six stages
+    } else {
+      write_out(cur_m0, cur_n0);
+      if (R != nullptr) __syncthreads();  // the next tile's residual DMA refills the C tile
+    }
   }
 }
 
