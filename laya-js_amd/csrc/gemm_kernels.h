@@ -752,6 +752,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       }
     }
   };
+  // scales of the stage's W rows, read from the ring ahead of store_b
+  uint32_t szv[B_LD];
+  auto read_sz = [&](int buf) __attribute__((always_inline)) {
+    if constexpr (QRING) {
+#pragma unroll
+      for (int i = 0; i < B_LD; i++) szv[i] = Zs[buf * NT + ((tid + i * NT) >> 3)];
+    }
+  };
   auto store_b = [&](int buf, const BRegs& br) {
     uint16_t* b = Bs + buf * BN * BK;
 #pragma unroll
@@ -760,7 +768,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if constexpr (QB == 0) {
         *(uint4v*)(b + swz(r, c)) = br.v[i];
       } else if constexpr (QRING) {
-        const uint32_t sz = Zs[buf * NT + r];  // the stage's ring slot is its W buffer
+        const uint32_t sz = szv[i];  // from the stage's ring slot (its W buffer)
         *(uint4v*)(b + swz(r, c)) = dequant8<QB, AFF, false, BF16>(br.v[i].x, br.v[i].y, sz & 0xffffu, sz >> 16,
                                                                     0.f, 0.f);
       } else {
@@ -1176,6 +1184,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       zr[(SP + 1) & 1] = load_sz(n3, k3b);
     }
     const uint16_t* b = Bs + (g & 1) * BN * BK;
+    read_sz((g + 1) & 1);
     uint4v bf[KS][TN];
 #pragma unroll
     for (int s = 0; s < KS; s++)
@@ -1194,7 +1203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // stores follow every load; the W staging for the next stage goes last
     constexpr int NVMEM = TM * KS + B_LD + NZ, NPAIR = KS * TN, WOS = WO ? WO_PS : 0;
     static_assert(NVMEM + 2 + WOS <= NPAIR, "write-out stores after the loads");
-    __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, TN + (QRING ? B_LD : 0), 0);
 #pragma unroll
     for (int p = 0; p < NPAIR; p++) {
       if (p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
@@ -1235,6 +1244,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       Zs[tid] = z0;
       Zs[NT + tid] = z1;
       __syncthreads();
+      read_sz(0);
     }
     store_b(0, B0);
     load_a(tile_m0(i1), k1, A1);
