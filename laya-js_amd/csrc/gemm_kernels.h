@@ -79,19 +79,33 @@ __device__ __forceinline__ uint4v dequant8(uint32_t w0, uint32_t w1, uint32_t sb
                                            float zf) {
   uint32_t out[4];
   if constexpr (!SF32 && !BF16) {
-    f16 s, z;
-    uint16_t sb = (uint16_t)sbits, zb = (uint16_t)zbits;
-    __builtin_memcpy(&s, &sb, 2);
-    __builtin_memcpy(&z, &zb, 2);
+    // Two codes per 32-bit word, each as the f16 1024 + c (c in 0..255 or
+    // 0..15 is the low mantissa bits under the exponent of 1024, exact), then
+    // one packed subtraction gives the code as f16 exactly and one packed
+    // multiply (symmetric) or fma (affine) rounds q*s (+ z) once.
+    const half2v s2 = __builtin_bit_cast(half2v, (sbits & 0xffffu) * 0x10001u);
+    const half2v z2 = __builtin_bit_cast(half2v, (zbits & 0xffffu) * 0x10001u);
+    uint32_t pr[4];  // value pairs (2e, 2e + 1) in the low bits of each half
+    if constexpr (QB == 8) {
+      // byte b of w0:w1 -> half (b & 1) of pair b / 2
+      pr[0] = __builtin_amdgcn_perm(0u, w0, 0x0c010c00u);
+      pr[1] = __builtin_amdgcn_perm(0u, w0, 0x0c030c02u);
+      pr[2] = __builtin_amdgcn_perm(0u, w1, 0x0c010c00u);
+      pr[3] = __builtin_amdgcn_perm(0u, w1, 0x0c030c02u);
+    } else {
+      // nibble e of w0 (e even: low nibble of byte e / 2)
+      const uint32_t lo = w0 & 0x0f0f0f0fu, hi = (w0 >> 4) & 0x0f0f0f0fu;
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      f16 q0 = (f16)(float)qcode<QB, AFF>(w0, w1, e), q1 = (f16)(float)qcode<QB, AFF>(w0, w1, e + 1);
-      f16 r0 = AFF ? __builtin_fmaf16(q0, s, z) : (f16)(q0 * s);
-      f16 r1 = AFF ? __builtin_fmaf16(q1, s, z) : (f16)(q1 * s);
-      uint16_t b0, b1;
-      __builtin_memcpy(&b0, &r0, 2);
-      __builtin_memcpy(&b1, &r1, 2);
-      out[e >> 1] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+      for (int p = 0; p < 4; p++) pr[p] = __builtin_amdgcn_perm(hi, lo, 0x0c040c00u + 0x00010001u * p);
+    }
+    // signed codes are stored offset by 2^(QB-1): q + 2^(QB-1) = c ^ 2^(QB-1)
+    constexpr uint32_t flip = AFF ? 0u : (QB == 8 ? 0x00800080u : 0x00080008u);
+    constexpr _Float16 base = AFF ? (_Float16)1024 : (_Float16)(1024 + (1 << (QB - 1)));
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const half2v q2 = __builtin_bit_cast(half2v, (pr[p] ^ flip) | 0x64006400u) - half2v{base, base};
+      const half2v r2 = AFF ? __builtin_elementwise_fma(q2, s2, z2) : q2 * s2;
+      out[p] = __builtin_bit_cast(uint32_t, r2);
     }
   } else {
     const float s = SF32 ? sf : f16_bits_to_f32((uint16_t)sbits);
