@@ -183,10 +183,14 @@ int hb_graph_destroy(uintptr_t ctx, uintptr_t exec);
 int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintptr_t w, uintptr_t bias, uintptr_t resid,
               int64_t ldr, uintptr_t y, int64_t ldy, int64_t M, int64_t N, int64_t K, unsigned flags);
 /*  HB_X_PANEL / HB_Y_PANEL (hb_linear and hb_qlinear): x read from / y
- *  written in panel order.  Taken by the large-M kernel only: dt f16 or
- *  bf16, M >= 4096, K % 64 == 0, 16-byte aligned operands; a panel-order y
- *  also needs N % 16 == 0 and no residual.  Other calls fail.  The
- *  arithmetic is the same as with row-major operands, bit for bit. */
+ *  written in panel order.  Taken by two kernels: dt f16 or bf16,
+ *  K % 64 == 0, 16-byte aligned operands, and either M >= 4096 (the large-M
+ *  kernel), or, for hb_linear only, a call that takes the small-M slab
+ *  kernel: 64 * K * (2 with GeGLU) <= 160 KiB and
+ *  ceil(N / 32) * ceil(M / 128) <= the device's CUs (hb_device_info "cus").
+ *  A panel-order y also needs N % 16 == 0 and no residual.  Other calls
+ *  fail.  The arithmetic is the same as with row-major operands, bit for
+ *  bit. */
 
 /* The attention block's q / k / v projection fused with its layout glue
  * and RoPE: y = x . w^T for the stacked projection w [3*H*64, K] (no bias,

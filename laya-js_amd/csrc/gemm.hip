@@ -159,15 +159,17 @@ __global__ __launch_bounds__(256) void gemm_dot(int dt, const void* __restrict__
 
 static bool dot_shape(int64_t M, int64_t N, int64_t K) { return M * N <= 16384 && K >= 256; }
 
-// Panel-order operands (HB_X_PANEL / HB_Y_PANEL) need the large-M MFMA kernel
-// with K % 64 == 0; a panel-order Y also a width of whole 16-column blocks
-// and no residual.
-static void check_panel(unsigned flags, bool mfma, int64_t M, int64_t N_out, int64_t K, bool resid, const char* op) {
+// Panel-order operands (HB_X_PANEL / HB_Y_PANEL) need K % 64 == 0 and one of
+// the two kernels that take them: the large-M one (M >= 4096) or, for 16-bit
+// weights, the small-M slab kernel (`slab`: the call takes it); a panel-order
+// Y also a width of whole 16-column blocks and no residual.
+static void check_panel(unsigned flags, bool mfma, bool slab, int64_t M, int64_t N_out, int64_t K, bool resid,
+                        const char* op) {
   if (!(flags & (HB_X_PANEL | HB_Y_PANEL))) return;
-  if (!mfma || !arow_path(M) || K % 64 != 0)
+  if (!mfma || !(arow_path(M) || slab) || K % 64 != 0)
     throw std::runtime_error(std::string(op) +
-                             ": panel-order operands need f16/bf16, M >= 4096, K % 64 == 0 and 16-byte aligned "
-                             "operands");
+                             ": panel-order operands need f16/bf16, K % 64 == 0, 16-byte aligned operands and "
+                             "M >= 4096, or (16-bit weights) the small-M slab kernel");
   if ((flags & HB_Y_PANEL) && (N_out % 16 != 0 || resid))
     throw std::runtime_error(std::string(op) + ": a panel-order y needs out % 16 == 0 and no residual");
 }
@@ -202,7 +204,8 @@ extern "C" int hb_linear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintpt
   hipStream_t st = stream_of(ctx);
   bool mfma = (dt == HB_F16 || dt == HB_BF16) && K > 0 && K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 &&
               (!r || ldr % 8 == 0) && x % 16 == 0 && w % 16 == 0 && y % 16 == 0 && (!r || resid % 16 == 0);
-  check_panel(flags, mfma, M, N, K, r != nullptr, "hb_linear");
+  check_panel(flags, mfma, !arow_path(M) && slab_path(M, N, K, geglu, cu_count(ctx)), M, N, K, r != nullptr,
+              "hb_linear");
   const unsigned pan = flags & (HB_X_PANEL | HB_Y_PANEL);
   if (mfma) {
     QW qw{nullptr, nullptr, nullptr, 0, 1};
@@ -273,7 +276,7 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
   bool mfma = (dt == HB_F16 || dt == HB_BF16) && K > 0 && K % 8 == 0 && group % 8 == 0 && ldx % 8 == 0 &&
               ldy % 8 == 0 && (!r || ldr % 8 == 0) && x % 16 == 0 && y % 16 == 0 && (!r || resid % 16 == 0) &&
               qw % 8 == 0 && scales % 2 == 0 && zeros % 2 == 0;
-  check_panel(flags, mfma, M, N, K, r != nullptr, "hb_qlinear");
+  check_panel(flags, mfma, false, M, N, K, r != nullptr, "hb_qlinear");
   const unsigned pan = flags & (HB_X_PANEL | HB_Y_PANEL);
   if (mfma) {
     QW q{(const uint8_t*)qw, (const void*)scales, (const void*)zeros, G, group};

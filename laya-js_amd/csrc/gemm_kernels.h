@@ -439,7 +439,7 @@ template <int TN, int P, bool BF16, bool GEGLU>
 __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X, int64_t ldx,
                                                  const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
                                                  const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
-                                                 int64_t ldy, int M, int N, int K, int chunks) {
+                                                 int64_t ldy, int M, int N, int K, int chunks, int xpan, int ypan) {
   constexpr int TNO = GEGLU ? TN / 2 : TN;  // output column blocks
   constexpr int SR = 32 * TN;               // slab rows
   static_assert(!GEGLU || TN % 2 == 0, "GEGLU needs value and gate blocks");
@@ -450,11 +450,16 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
   const int n0 = nt * 32 * TNO;
   const int KB = K >> 6, S = K >> 4;  // 64-wide k blocks, k16 steps
   const int row = (mc * 4 + wave) * 32 + l32;  // this lane's output row
-  const int64_t xoff = (int64_t)(row < M ? row : M - 1) * ldx + 8 * lg;
+  // X row-major, or in panel order (xpan: 32-row x 16-column blocks of 1 KB
+  // in MFMA operand order, rows padded to a multiple of 32), where one
+  // fragment load reads one whole block; rows past the operand are clamped
+  const int mlim = xpan ? (M + 31) & ~31 : M, rc = row < mlim ? row : mlim - 1;
+  const int64_t xoff = xpan ? (int64_t)(rc >> 5) * 32 * K + (rc & 31) * 8 + 256 * lg : (int64_t)rc * ldx + 8 * lg;
+  const int xstep = xpan ? 512 : 16;  // elements per k16 step
 
   uint4v xf[P];
 #pragma unroll
-  for (int p = 0; p < P; p++) xf[p] = *(const uint4v*)(X + xoff + 16 * p);
+  for (int p = 0; p < P; p++) xf[p] = *(const uint4v*)(X + xoff + xstep * p);
   // epilogue inputs: the residual and the bias of the lane's 4-column groups
   // (8-byte loads where aligned: R rows are, ldr % 8 == 0; the bias may be a
   // view at any offset, and its gate half starts at N)
@@ -504,7 +509,7 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
       for (int j = 0; j < TN; j++) b[j] = wfrag(j, s0 + p);
 #pragma unroll
       for (int j = 0; j < TN; j++) acc[j] = mfma32<BF16>(b[j], xf[p], acc[j]);
-      if (s0 + P < S) xf[p] = *(const uint4v*)(X + xoff + 16 * (s0 + P + p));  // K longer than the registers
+      if (s0 + P < S) xf[p] = *(const uint4v*)(X + xoff + xstep * (s0 + P + p));  // K longer than the registers
     }
   }
 
@@ -546,7 +551,11 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
           o[e] = from_f<BF16>(to_f<BF16>(o[e]) + to_f<BF16>(r16));
         }
       }
-      uint16_t* yp = Y + (int64_t)row * ldy + col;
+      // row-major, or panel order (ypan: N % 16 == 0, so the 4 columns are
+      // whole and 8 bytes of one 16-byte chunk of a 1 KB block)
+      uint16_t* yp = ypan ? Y + ((int64_t)(row >> 5) * (N >> 4) + (col >> 4)) * 512 +
+                                (((col >> 3) & 1) * 32 + (row & 31)) * 8 + (col & 7)
+                          : Y + (int64_t)row * ldy + col;
       if (whole) {
         *(uint2v*)yp = uint2v{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
       } else {
@@ -1416,7 +1425,7 @@ void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64
 // 36, 32, 24, 16 and 4 that divides K/16.
 template <int TN, bool BF16, bool GEGLU>
 void launch_slab_t(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias,
-                   const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K) {
+                   const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K, unsigned pan) {
   constexpr int TNO = GEGLU ? TN / 2 : TN;
   const int tiles_n = (N + 32 * TNO - 1) / (32 * TNO), chunks = (M + 127) / 128;
   const size_t lds = (size_t)32 * TN * K * sizeof(uint16_t);
@@ -1427,7 +1436,8 @@ void launch_slab_t(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_
     once_per_device(attr, [&] {
       HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     });
-    kern<<<tiles_n * chunks, 256, lds, st>>>(x, ldx, w, bias, r, ldr, y, ldy, M, N, K, chunks);
+    kern<<<tiles_n * chunks, 256, lds, st>>>(x, ldx, w, bias, r, ldr, y, ldy, M, N, K, chunks,
+                                              (pan & HB_X_PANEL) ? 1 : 0, (pan & HB_Y_PANEL) ? 1 : 0);
   };
   if (S % 48 == 0) go(gemm_slab<TN, 48, BF16, GEGLU>);
   else if (S % 36 == 0) go(gemm_slab<TN, 36, BF16, GEGLU>);
@@ -1446,8 +1456,9 @@ inline bool slab_path(int64_t M, int64_t N_out, int64_t K, bool geglu, int cus) 
   return K % 64 == 0 && K * 32 * (geglu ? 2 : 1) * 2 <= 160 * 1024 && tiles_n * chunks <= cus;
 }
 
-// The large-M kernel runs for M >= 4096; it is the only one that takes
-// panel-order operands (the entry points check that before dispatching).
+// The large-M kernel runs for M >= 4096.  It and the small-M slab kernel
+// (16-bit weights) take panel-order operands; the entry points check that
+// the call takes one of them before dispatching.
 inline bool arow_path(int64_t M) { return M >= 4096; }
 
 template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
@@ -1467,10 +1478,11 @@ void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int
   else {
     if constexpr (QB == 0) {
       if (slab_path(M, N, K, GEGLU, cus)) {
-        launch_slab_t<GEGLU ? 2 : 1, BF16, GEGLU>(st, x, ldx, w, bias, r, ldr, y, ldy, M, N, K);
+        launch_slab_t<GEGLU ? 2 : 1, BF16, GEGLU>(st, x, ldx, w, bias, r, ldr, y, ldy, M, N, K, pan);
         return;
       }
     }
+    HB_REQUIRE(pan == 0, "hb_linear: panel-order operands on a kernel that does not take them");
     launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   }
 }

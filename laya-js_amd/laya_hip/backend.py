@@ -19,8 +19,9 @@ Design (MI355X-first, not a port of any reference backend):
   [B, H, L, D] view of it, so the encoder's transpose + reshape back to
   [B, L, H*D] (modernbert/src/index.ts:352) is free.
 - `layerNorm` and `geglu` of a pending linear are pending too.  When their
-  first consumer is a large-M linear layer (M >= 4096, 16-bit, K % 64 == 0)
-  they are written in panel order (laya_hip.h: 32 x 16 blocks in MFMA
+  first consumer is a linear layer that reads panel order (16-bit, K % 64 ==
+  0, and M >= 4096 or, with 16-bit weights, the small-M slab kernel) they
+  are written in panel order (laya_hip.h: 32 x 16 blocks in MFMA
   operand order), which the GEMM loads a whole block per instruction; any
   other reader gets a row-major copy (hb_panel_unpack).  Same values, bit
   for bit: only the addressing differs.
@@ -145,7 +146,15 @@ class HipTensor:
 
 # ------------------------------------------------------------------ pending work
 
-PANEL_MIN_M = 4096  # the large-M GEMM, the one kernel that takes panel-order operands
+PANEL_MIN_M = 4096  # the large-M GEMM; below it the small-M slab kernel also takes panel-order operands
+SLAB_LDS = 160 * 1024  # the slab kernel's LDS: 64 * K bytes per 32 output columns (x2 with GeGLU)
+
+
+def _slab_path(M: int, n_out: int, K: int, geglu: bool, cus: int) -> bool:
+    """hb_linear takes the small-M slab kernel (16-bit weights, M < 4096):
+    the conditions of slab_path in csrc/gemm_kernels.h."""
+    return (M < PANEL_MIN_M and K % 64 == 0 and 64 * K * (2 if geglu else 1) <= SLAB_LDS
+            and -(-n_out // 32) * -(-M // 128) <= cus)
 
 
 def _panel_rows(M: int) -> int:
@@ -154,8 +163,8 @@ def _panel_rows(M: int) -> int:
 
 class _PanelRows:
     """The value of a tensor, an [M, K] 16-bit matrix, held in panel order
-    (rows padded to a multiple of 32) in `st`, written for a large-M linear
-    layer.  Other readers get a row-major copy (HipBackend._ready): the
+    (rows padded to a multiple of 32) in `st`, written for a linear layer that
+    reads panel order.  Other readers get a row-major copy (HipBackend._ready): the
     LayerNorm it came from run again row-major (`norm`, same bits), or an
     unpack of the panel."""
 
@@ -173,7 +182,7 @@ class _PanelRows:
 
 class _PendingNorm:
     """layerNorm not yet launched (index.ts:216-217): row-major on first
-    use, or panel order when a large-M linear layer consumes it first."""
+    use, or panel order when a linear layer that reads it consumes it first."""
 
     def __init__(self, be, x, weight, bias, eps: float, dt: str):
         st, xp, rows, D, ld = be._rows(x)
@@ -234,16 +243,27 @@ class _PendingLinear:
         self.N = w.shape[0] if q is None else q[5]
         self.dtype = x.dtype
         M, K = self.x[1], self.x[2]
-        # the large-M MFMA kernel takes this launch (panel-order operands
-        # allowed): hb_linear / hb_qlinear's conditions on everything but the
-        # output and the residual, which are checked at launch
-        ok = x.dtype in ("f16", "bf16") and M >= PANEL_MIN_M and K % 64 == 0 and self.x[0] % 16 == 0
+        # the operand conditions of the MFMA kernels that take panel-order
+        # operands (hb_linear / hb_qlinear's, on everything but the output and
+        # the residual, which are checked at launch); arow_ok: the large-M one
+        ok = x.dtype in ("f16", "bf16") and K % 64 == 0 and self.x[0] % 16 == 0
         if q is None:
             ok = ok and self.wp % 16 == 0
         else:
             sp, zp, bits, group, mode = self.q
             ok = ok and self.wp % 8 == 0 and sp % 2 == 0 and zp % 2 == 0 and group % 8 == 0
-        self.arow_ok = ok
+        self.operands_ok = ok
+        self.arow_ok = ok and M >= PANEL_MIN_M
+
+    def takes_panel(self, epi: int) -> bool:
+        """The launch with epilogue `epi` takes a kernel that reads and
+        writes panel order: the large-M one, or (16-bit weights) the slab."""
+        if self.arow_ok:
+            return True
+        M, K = self.x[1], self.x[2]
+        geglu = bool(epi & F.HB_EPI_GEGLU)
+        n_out = self.N // 2 if geglu else self.N
+        return self.operands_ok and self.q is None and _slab_path(M, n_out, K, geglu, self.be.cus)
 
     def fork(self, epi: int) -> "_PendingLinear":
         """The same product with epilogue `epi` (own references)."""
@@ -272,8 +292,9 @@ class _PendingLinear:
             flags |= F.HB_EPI_RESID
         tmp = None
         if self.panel is not None:
-            if resid[0] and (resid[0] % 16 or resid[1] % 8):
-                # a residual the large-M kernel cannot read: unpack x first
+            if (resid[0] and (resid[0] % 16 or resid[1] % 8)) or not self.takes_panel(flags):
+                # a residual the MFMA kernels cannot read, or a launch that
+                # takes a kernel without panel operands: unpack x first
                 tmp = be._malloc(M * K * 2)
                 be._call("linear", "hb_panel_unpack", be.ctx, xp, tmp.ptr, K, M, K)
                 xp, ldx = tmp.ptr, K
@@ -391,8 +412,8 @@ class _PendingSdpa:
     """sdpa not yet launched (index.ts:230-237).  The result and the views
     taken of it (transpose / reshape keep their strides over the output's
     physical [B, Lq, H, D] storage) share this object; the first reader
-    launches it: row-major for most, or in panel order for a large-M linear
-    layer reading the contiguous [B*Lq, H*D] view (modernbert's merged
+    launches it: row-major for most, or in panel order for a linear layer
+    that reads panel order reading the contiguous [B*Lq, H*D] view (modernbert's merged
     heads into attn Wo).  Holds a reference on every operand's storage."""
 
     def __init__(self, be, args, refs, panel_ok: bool):
@@ -504,6 +525,7 @@ class HipBackend:
         self._blocks: dict[int, list[int]] = {}
         self._capture_held: Optional[list] = None  # blocks disposed while a capture records
         self._capture_summaries: Optional[set] = None  # summaries already enqueued into the recording
+        self._cus: Optional[int] = None  # compute units, read once (HipBackend.cus)
         self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "linear_fused_qkv": 0, "sdpa": 0,
                       "sdpa_fused_rope": 0, "copies": 0, "panel_unpacks": 0}
 
@@ -561,6 +583,13 @@ class HipBackend:
         buf = F.C.create_string_buffer(1024)
         self._call("deviceInfo", "hb_device_info", self.ctx, buf, 1024)
         return json.loads(buf.value.decode())
+
+    @property
+    def cus(self) -> int:
+        """The device's compute units (the small-M GEMM's grid condition)."""
+        if self._cus is None:
+            self._cus = int(self.device_info()["cus"])
+        return self._cus
 
     # Blocks of disposed tensors wait in `_blocks` (size class -> pointers)
     # for the next allocation of the same class, without a call into the
@@ -683,13 +712,13 @@ class HipBackend:
         return t
 
     def _as_panel(self, x: HipTensor) -> Optional[_PanelRows]:
-        """x's value in panel order for a large-M linear layer: already there,
+        """x's value in panel order for a linear layer that reads it: already there,
         or written so now if x is a pending layerNorm or a pending GeGLU
         linear that can write it; else None."""
         lz = x._lazy
         if isinstance(lz, _PanelRows):
             return lz
-        if isinstance(lz, _PendingNorm) and lz.panel_ok and lz.rows >= PANEL_MIN_M and lz.D % 64 == 0:
+        if isinstance(lz, _PendingNorm) and lz.panel_ok and lz.D % 64 == 0:
             st = self._malloc(_panel_rows(lz.rows) * lz.D * 2)
             dtx, xp, ld, dtw, wp, bp = lz.args
             self._call("layerNorm", "hb_layernorm_panel", self.ctx, dtx, xp, ld, dtw, wp, bp, st.ptr, lz.rows, lz.D,
@@ -702,7 +731,8 @@ class HipBackend:
             lz.release()
             x._lazy = _PanelRows(st, lz.M, lz.K)
             return x._lazy
-        if (isinstance(lz, _PendingLinear) and lz.epi == F.HB_EPI_GEGLU and lz.arow_ok and lz.n_out % 64 == 0):
+        if (isinstance(lz, _PendingLinear) and lz.epi == F.HB_EPI_GEGLU and lz.takes_panel(lz.epi)
+                and lz.n_out % 64 == 0):
             M = lz.x[1]
             st = self._malloc(_panel_rows(M) * lz.n_out * 2)
             self.stats["linear"] += 1
@@ -1396,9 +1426,16 @@ class HipBackend:
         return self._track(HipTensor(x.shape[:-1] + (w.shape[0],), dt, None, lazy=pend))
 
     def _panel_for(self, x: HipTensor, w: Optional[HipTensor] = None, q=None) -> Optional[_PanelRows]:
-        """The panel-order form of x when this linear layer takes the large-M
-        kernel (weights side checked here, x side by _as_panel)."""
-        if x.dtype not in ("f16", "bf16") or not x.shape or _numel(x.shape[:-1]) < PANEL_MIN_M:
+        """The panel-order form of x when this linear layer takes a kernel
+        that reads it: the large-M one, or for 16-bit weights the small-M slab
+        kernel as the launch without an epilogue takes it (weights side
+        checked here, x side by _as_panel; a launch that ends up taking
+        another kernel unpacks x)."""
+        if x.dtype not in ("f16", "bf16") or not x.shape:
+            return None
+        M = _numel(x.shape[:-1])
+        if M < PANEL_MIN_M and (q is not None or w is None
+                                or not _slab_path(M, w.shape[0], x.shape[-1], False, self.cus)):
             return None
         if x._lazy is None or isinstance(x._lazy, _PendingRope):
             return None
@@ -1539,8 +1576,8 @@ class HipBackend:
             mp = self._ptr(mc)
             refs.append(mc._st.retain())
         info = self._mask_info(mc, ms, B, Lq, Lk) if mc is not None else 0
-        # hb_sdpa_panel's conditions (its MFMA path), for a large-M consumer
-        panel_ok = (dt in ("f16", "bf16") and D == 64 and Lk > 0 and B * Lq >= PANEL_MIN_M and (H * D) % 64 == 0
+        # hb_sdpa_panel's conditions (its MFMA path), for a consumer that reads panel order
+        panel_ok = (dt in ("f16", "bf16") and D == 64 and Lk > 0 and (H * D) % 64 == 0
                     and all(p % 16 == 0 for p in (qp, kp, vp)) and all(st_[3] == 1 for st_ in (qs, ks, vs))
                     and all(st_[i] % 8 == 0 for st_ in (qs, ks, vs) for i in range(3))
                     and (ms is None or ms[1] == 0) and (Lk + 63) // 64 <= 1024)

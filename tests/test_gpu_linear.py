@@ -291,3 +291,64 @@ def test_small_m_slab_edges_and_bits_equal_large_m(b, dtype):
         np.testing.assert_array_equal(np.asarray(b.read(y).data), big[:M])
         for t in (X, Wt, Bfull, R, y, XB, RB, yb) + ((Bt,) if Bt is not None else ()):
             b.dispose(t)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_small_m_slab_takes_panel_operands(b, dtype):
+    """The small-M slab kernel reads x in panel order (HB_X_PANEL) and writes
+    a GeGLU output in panel order (HB_Y_PANEL), through the C ABI: bit for bit
+    the row-major results, for row counts that are not multiples of 32 (the
+    panel's padding rows) and a K longer than the registers (1152).  Calls
+    that take the 128 x 128 kernel, and small-M quantized calls, refuse
+    panel operands."""
+    from laya_hip import ffi as F
+    rng = np.random.default_rng(31)
+    dt = F.HB_F16 if dtype == "f16" else F.HB_BF16
+
+    def bits(ptr, n):
+        out = np.empty(n, np.uint16)
+        b.n.call("read", "hb_download", b.ctx, out.ctypes.data, ptr, out.nbytes)
+        return out
+
+    for (M, N2, K, geglu, with_bias) in [(1, 768, 768, False, False), (33, 2304, 768, True, True),
+                                         (100, 768, 1152, False, True), (128, 2304, 768, False, False),
+                                         (128, 2304, 768, True, False)]:
+        print(f"slab panel M={M} N={N2} K={K} geglu={geglu} {dtype}", flush=True)
+        No = N2 // 2 if geglu else N2
+        x = rounded(rng.standard_normal((M, K)), dtype)
+        w = rounded(rng.normal(0, 0.05, (N2, K)), dtype)
+        bias = rounded(rng.standard_normal(N2), dtype)
+        X, Wt, Bt = (b.fromHost(to_host(a, dtype)) for a in (x, w, bias))
+        xp, wp, bp = b._ptr(X), b._ptr(Wt), (b._ptr(Bt) if with_bias else 0)
+        flags = (F.HB_EPI_GEGLU if geglu else 0) | (F.HB_EPI_BIAS if with_bias else 0)
+        Mp = (M + 31) // 32 * 32
+        ref = b._malloc(M * No * 2)
+        b.n.call("linear", "hb_linear", b.ctx, dt, xp, K, wp, bp, 0, 0, ref.ptr, No, M, No, K, flags)
+        want = bits(ref.ptr, M * No)
+        packed = b._malloc(Mp * K * 2)
+        b.n.call("pack", "hb_panel_pack", b.ctx, xp, K, packed.ptr, M, K)
+        y = b._malloc(M * No * 2)
+        b.n.call("linear", "hb_linear", b.ctx, dt, packed.ptr, K, wp, bp, 0, 0, y.ptr, No, M, No, K,
+                 flags | F.HB_X_PANEL)
+        np.testing.assert_array_equal(bits(y.ptr, M * No), want)
+        yp = b._malloc(Mp * No * 2)
+        b.n.call("linear", "hb_linear", b.ctx, dt, packed.ptr, K, wp, bp, 0, 0, yp.ptr, No, M, No, K,
+                 flags | F.HB_X_PANEL | F.HB_Y_PANEL)
+        b.n.call("unpack", "hb_panel_unpack", b.ctx, yp.ptr, y.ptr, No, M, No)
+        np.testing.assert_array_equal(bits(y.ptr, M * No), want)
+        for m in (ref, packed, y, yp):
+            m.release()
+        for t in (X, Wt, Bt):
+            b.dispose(t)
+    # 2048 rows of a 2304-wide product take the 128 x 128 kernel: refused
+    x = b._malloc(2048 * 768 * 2)
+    w = b._malloc(2304 * 768 * 2)
+    y = b._malloc(2048 * 2304 * 2)  # sized for the call, which is refused before any launch
+    with pytest.raises(F.HipError, match="panel-order operands"):
+        b.n.call("linear", "hb_linear", b.ctx, dt, x.ptr, 768, w.ptr, 0, 0, 0, y.ptr, 2304, 2048, 2304, 768,
+                 F.HB_X_PANEL)
+    with pytest.raises(F.HipError, match="panel-order operands"):  # quantized weights below 4096 rows
+        b.n.call("quantizedLinear", "hb_qlinear", b.ctx, dt, x.ptr, 768, w.ptr, w.ptr, 0, 0, 0, 0, x.ptr, 768,
+                 128, 768, 768, 8, 64, 0, F.HB_X_PANEL)
+    for m in (x, w, y):
+        m.release()
