@@ -147,12 +147,10 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   }
 }
 
-// 4 mask bytes (any nonzero byte is true) -> 4 bits, byte i -> bit i.
-__device__ __forceinline__ uint32_t mask_bits(uint32_t w) {
-  // bit 7 of each byte set iff the byte is nonzero (no carries between bytes)
-  const uint32_t nz = (((w & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w) & 0x80808080u;
-  // bytes' bit 0 (nz >> 7) gathered into bits 24..27 by one multiply
-  return ((nz >> 7) * 0x01020408u) >> 24;
+// 4 mask bytes (any nonzero byte is true): bit 7 of each byte set iff the
+// byte is nonzero (no carries between bytes)
+__device__ __forceinline__ uint32_t mask_nz(uint32_t w) {
+  return (((w & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w) & 0x80808080u;
 }
 
 // Cross-lane exchanges for the 4 lanes that hold one query (lane, lane ^ 16,
@@ -290,10 +288,12 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
   }
   auto tile_needed = [&](int kt) -> bool { return cls_row[kt] != 0; };
   auto wave_class = [&](int kt) -> int { return (cls_row[kt] >> (2 * wave)) & 3; };
+  // (the same in every lane: read from the class row in LDS, made
+  // wave-uniform so that the tile's address arithmetic is scalar)
   auto next_tile = [&](int kt) -> int {
     kt++;
     while (kt < nkt && !tile_needed(kt)) kt++;
-    return kt;
+    return __builtin_amdgcn_readfirstlane(kt);
   };
   __syncthreads();  // the class row is complete
 
@@ -306,16 +306,22 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
   const int vc = tid & 7, vj = 2 * ((tid & 255) >> 3);
   uint4v pr0, pr1;  // K threads: chunks kc and kc + 4 of row kr; V threads: keys vj and vj + 1
   float2 kcs[8];    // RoPE cos / sin of this thread's K row (fused RoPE)
+  // The tile's first row is a scalar address (k0 is wave-uniform); a
+  // thread's row within the tile adds a 24-bit product (row < 64, a row
+  // stride below 2^24 elements: the host's condition for this kernel).
   auto prefetch = [&](int kt) {
     const int k0 = kt * kBK;
     if (kpart) {
-      load_pair(Kb + (int64_t)(k0 + kr) * ks.s[2], k0 + kr < Lk, kc, pr0, pr1);
-      if (tabk != nullptr && k0 + kr < Lk) load_cs(tabk, k0 + kr, kc, kcs);
+      const uint16_t* kb = Kb + (int64_t)k0 * ks.s[2];
+      load_pair(kb + __umul24(kr, (uint32_t)ks.s[2]), k0 + kr < Lk, kc, pr0, pr1);
+      if (tabk != nullptr && k0 + kr < Lk) load_cs(tabk + (int64_t)k0 * 32, kr, kc, kcs);
     } else {
+      const uint16_t* vb = Vb + (int64_t)k0 * vs.s[2] + vc * 8;
+      const uint32_t vo = __umul24(vj, (uint32_t)vs.s[2]);
       pr0 = uint4v{0, 0, 0, 0};
       pr1 = uint4v{0, 0, 0, 0};
-      if (k0 + vj < Lk) pr0 = *(const uint4v*)(Vb + (int64_t)(k0 + vj) * vs.s[2] + vc * 8);
-      if (k0 + vj + 1 < Lk) pr1 = *(const uint4v*)(Vb + (int64_t)(k0 + vj + 1) * vs.s[2] + vc * 8);
+      if (k0 + vj < Lk) pr0 = *(const uint4v*)(vb + vo);
+      if (k0 + vj + 1 < Lk) pr1 = *(const uint4v*)(vb + vo + (uint32_t)vs.s[2]);
     }
   };
 
@@ -480,14 +486,26 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
 #pragma unroll
           for (int t = 0; t < 2; t++) {
             const int kbase = k0 + 32 * t + 8 * g;  // this lane's 8 contiguous keys
-            // bit e of vis: key kbase + e is visible (mask byte nonzero, key < Lk)
-            uint32_t vis = 0xffu;
-            if (mask != nullptr) vis = mask_bits(mw[qb][t].x) | (mask_bits(mw[qb][t].y) << 4);
+            // bit 7 of byte e % 4 of word e / 4: key kbase + e is visible
+            // (mask byte nonzero, key < Lk)
+            uint32_t vx = 0x80808080u, vy = 0x80808080u;
+            if (mask != nullptr) {
+              vx = mask_nz(mw[qb][t].x);
+              vy = mask_nz(mw[qb][t].y);
+            }
             const int left = Lk - kbase;
-            if (left < 8) vis &= left > 0 ? (1u << left) - 1u : 0u;
+            if (left < 8) {
+              vx &= left >= 4 ? ~0u : (left <= 0 ? 0u : 0xffffffffu >> (8 * (4 - left)));
+              vy &= left <= 4 ? 0u : 0xffffffffu >> (8 * (8 - left));
+            }
+            // a hidden score becomes -inf: the byte's bit 7 sign-extended to
+            // a word mask, one bit-field insert per score
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-              st[qb][2 * t + (e >> 2)][e & 3] = (vis >> e) & 1u ? st[qb][2 * t + (e >> 2)][e & 3] : -INFINITY;
+            for (int e = 0; e < 8; e++) {
+              const uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)(e < 4 ? vx : vy), 8 * (e & 3) + 7, 1);
+              const float sv = st[qb][2 * t + (e >> 2)][e & 3];
+              st[qb][2 * t + (e >> 2)][e & 3] = __uint_as_float((__float_as_uint(sv) & m) | (~m & 0xff800000u));
+            }
           }
         }
         float mx = -INFINITY;
@@ -661,7 +679,8 @@ static void sdpa_impl(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uin
               q % 16 == 0 && k % 16 == 0 && v % 16 == 0 && o % 8 == 0 && qs[2] % 8 == 0 && ks[2] % 8 == 0 &&
               vs[2] % 8 == 0 && qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 &&
               vs[0] % 8 == 0 && vs[1] % 8 == 0 && os[0] % 4 == 0 && os[1] % 4 == 0 && os[2] % 4 == 0 &&
-              (mask == 0 || ms[1] == 0) && (Lk + kBK - 1) / kBK <= kMaxKeyTiles;
+              (mask == 0 || ms[1] == 0) && (Lk + kBK - 1) / kBK <= kMaxKeyTiles && ks[2] < (1 << 24) &&
+              vs[2] < (1 << 24);
   if (pK > 0)
     HB_REQUIRE(fast && o % 16 == 0 && pK == H * D,
                "hb_sdpa_panel: needs the MFMA path (f16/bf16, D = 64, aligned operands, mask not varying over heads)");
