@@ -415,9 +415,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
 // ------------------------------------------------------------------ small-M MFMA kernel
 
 // Small-M GEMM for 16-bit weights (M < 4096, K % 64 == 0): weight-stationary,
-// one memory round trip.  A block of four waves owns a slab of 32*TN W rows
-// (the output columns n0 .. n0 + 32*TNO, and with GeGLU their gate rows too)
-// and 128 rows of X, one 32-row block per wave.  Everything a wave needs is
+// one memory round trip.  A block of two or four waves owns a slab of
+// 32*TN W rows (the output columns n0 .. n0 + 32*TNO, and with GeGLU their
+// gate rows too) and one 32-row block of X per wave.  Everything a wave needs is
 // requested at once before anything is waited for: its X fragments for P k16
 // steps (P = K/16 when that fits in registers), its residual and bias values,
 // and its share of the whole slab, which goes to LDS with direct-to-LDS loads
@@ -445,11 +445,12 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
   static_assert(!GEGLU || TN % 2 == 0, "GEGLU needs value and gate blocks");
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lg = lane >> 5;
+  const int nw = blockDim.x >> 6;  // waves per block (2 or 4): 32 rows of X each
   const int t = xcd_tile(blockIdx.x, gridDim.x);
   const int nt = t / chunks, mc = t - nt * chunks;
   const int n0 = nt * 32 * TNO;
   const int KB = K >> 6, S = K >> 4;  // 64-wide k blocks, k16 steps
-  const int row = (mc * 4 + wave) * 32 + l32;  // this lane's output row
+  const int row = (mc * nw + wave) * 32 + l32;  // this lane's output row
   // X row-major, or in panel order (xpan: 32-row x 16-column blocks of 1 KB
   // in MFMA operand order, rows padded to a multiple of 32), where one
   // fragment load reads one whole block; rows past the operand are clamped
@@ -475,10 +476,10 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
       rb[j][g] = bvec && col + 4 <= N ? *(const uint2v*)(bias + col) : uint2v{0, 0};
       rbg[j][g] = GEGLU && bvec && col + 4 <= N ? *(const uint2v*)(bias + N + col) : uint2v{0, 0};
     }
-  // the slab: DMA instruction q (of wave q % 4) fills block q, i.e. slab rows
+  // the slab: DMA instruction q (of wave q % nw) fills block q, i.e. slab rows
   // 8 * (q / KB) + lane / 8, k block q % KB; lane l fetches chunk (l%8) ^ (row%8)
   const int nq = (SR / 8) * KB;
-  for (int q = wave; q < nq; q += 4) {
+  for (int q = wave; q < nq; q += nw) {
     const int rb8 = q / KB, kb = q - rb8 * KB;
     const int r = rb8 * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
     const bool gate = GEGLU && r >= SR / 2;
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
   }
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): everything above has landed
   __syncthreads();
-  if ((mc * 4 + wave) * 32 >= M) return;  // a wave past the last row (after the barrier: its DMA share is done)
+  if ((mc * nw + wave) * 32 >= M) return;  // a wave past the last row (after the barrier: its DMA share is done)
 
   // W fragment of column block j, k16 step s (slab row 32 j + l32)
   auto wfrag = [&](int j, int s) __attribute__((always_inline)) -> uint4v {
@@ -1420,14 +1421,25 @@ void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64
                                (pan & HB_Y_PANEL) ? 1 : 0, qk);
 }
 
-// Small-M launcher for 16-bit weights: slabs of 32 (GeGLU: 64) W rows, 128
-// rows of X per block.  P (X steps held in registers) is the largest of 48,
-// 36, 32, 24, 16 and 4 that divides K/16.
+// Waves per slab block (each takes 32 rows of X): two when those blocks fit
+// one per CU, else four.  A CU's loads bound the kernel, so a launch spread
+// over more CUs finishes sooner although X and the slabs are then read by
+// more blocks (the k16 order per output is the same for any count).  One
+// wave per block, which leaves a wave the whole slab to fetch, measured
+// slower for the 64-row GeGLU slabs and no faster elsewhere.
+inline int slab_waves(int64_t M, int64_t tiles_n, int cus) {
+  return tiles_n * ((M + 63) / 64) <= cus ? 2 : 4;
+}
+
+// Small-M launcher for 16-bit weights: slabs of 32 (GeGLU: 64) W rows, 64
+// or 128 rows of X per block (slab_waves).  P (X steps held in registers)
+// is the largest of 48, 36, 32, 24, 16 and 4 that divides K/16.
 template <int TN, bool BF16, bool GEGLU>
-void launch_slab_t(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias,
+void launch_slab_t(hipStream_t st, int cus, const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias,
                    const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K, unsigned pan) {
   constexpr int TNO = GEGLU ? TN / 2 : TN;
-  const int tiles_n = (N + 32 * TNO - 1) / (32 * TNO), chunks = (M + 127) / 128;
+  const int tiles_n = (N + 32 * TNO - 1) / (32 * TNO);
+  const int nw = slab_waves(M, tiles_n, cus), chunks = (M + 32 * nw - 1) / (32 * nw);
   const size_t lds = (size_t)32 * TN * K * sizeof(uint16_t);
   HB_REQUIRE(lds <= 160 * 1024, "hb_linear: weight slab too large for LDS");
   const int S = K / 16;
@@ -1436,7 +1448,7 @@ void launch_slab_t(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_
     once_per_device(attr, [&] {
       HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     });
-    kern<<<tiles_n * chunks, 256, lds, st>>>(x, ldx, w, bias, r, ldr, y, ldy, M, N, K, chunks,
+    kern<<<tiles_n * chunks, 64 * nw, lds, st>>>(x, ldx, w, bias, r, ldr, y, ldy, M, N, K, chunks,
                                               (pan & HB_X_PANEL) ? 1 : 0, (pan & HB_Y_PANEL) ? 1 : 0);
   };
   if (S % 48 == 0) go(gemm_slab<TN, 48, BF16, GEGLU>);
@@ -1478,7 +1490,7 @@ void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int
   else {
     if constexpr (QB == 0) {
       if (slab_path(M, N, K, GEGLU, cus)) {
-        launch_slab_t<GEGLU ? 2 : 1, BF16, GEGLU>(st, x, ldx, w, bias, r, ldr, y, ldy, M, N, K, pan);
+        launch_slab_t<GEGLU ? 2 : 1, BF16, GEGLU>(st, cus, x, ldx, w, bias, r, ldr, y, ldy, M, N, K, pan);
         return;
       }
     }

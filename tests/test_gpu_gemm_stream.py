@@ -99,25 +99,30 @@ def test_streamed_tiles_equal_single_tile_rows(b, dtype, M, N, K, geglu, bias, r
             b.dispose(t)
 
 
+@pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_streamed_panel_output_equals_row_major(b, dtype):
+def test_streamed_panel_output_equals_row_major(b, dtype, bias):
     """The GeGLU linear with its output in panel order (streamed, as the
-    encoder's Wi runs) equals the row-major output bit for bit, with x
-    row-major and in panel order."""
-    print(f"streamed GeGLU panel output {dtype}", flush=True)
+    encoder's Wi runs: an interior tile's GELU products are formed while the
+    next tile computes) equals the row-major output (every GELU in the
+    epilogue) bit for bit, with x row-major and in panel order, with and
+    without a bias."""
+    print(f"streamed GeGLU panel output {dtype} bias={bias}", flush=True)
     M, N, K = 16384, 2304, 768
     rng = np.random.default_rng(5)
     dt = F.HB_F16 if dtype == "f16" else F.HB_BF16
     x = rounded(rng.standard_normal((M, K)), dtype)
     w = rounded(rng.normal(0, 0.03, (N, K)), dtype)
     X, Wt = b.fromHost(to_host(x, dtype)), b.fromHost(to_host(w, dtype))
+    Bt = b.fromHost(to_host(rounded(rng.standard_normal(N), dtype), dtype)) if bias else None
     xp, wp = b._ptr(X), b._ptr(Wt)
-    rowmajor = _linear(b, dt, xp, M, K, wp, N, geglu=True)
+    bp = b._ptr(Bt) if bias else 0
+    rowmajor = _linear(b, dt, xp, M, K, wp, N, bp, geglu=True)
     want = _bits(b, rowmajor.ptr, M * (N // 2))
     packed = b._malloc(M * K * 2)
     b.n.call("pack", "hb_panel_pack", b.ctx, xp, K, packed.ptr, M, K)
     for src, flags in ((xp, 0), (packed.ptr, F.HB_X_PANEL)):
-        yp = _linear(b, dt, src, M, K, wp, N, geglu=True, flags=flags | F.HB_Y_PANEL)
+        yp = _linear(b, dt, src, M, K, wp, N, bp, geglu=True, flags=flags | F.HB_Y_PANEL)
         out = b._malloc(M * (N // 2) * 2)
         b.n.call("unpack", "hb_panel_unpack", b.ctx, yp.ptr, out.ptr, N // 2, M, N // 2)
         np.testing.assert_array_equal(_bits(b, out.ptr, M * (N // 2)), want)
@@ -125,5 +130,6 @@ def test_streamed_panel_output_equals_row_major(b, dtype):
         out.release()
     packed.release()
     rowmajor.release()
-    b.dispose(X)
-    b.dispose(Wt)
+    for t in (X, Wt, Bt):
+        if t is not None:
+            b.dispose(t)
