@@ -1421,14 +1421,15 @@ void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64
                                (pan & HB_Y_PANEL) ? 1 : 0, qk);
 }
 
-// Waves per slab block (each takes 32 rows of X): two when those blocks fit
-// one per CU, else four.  A CU's loads bound the kernel, so a launch spread
-// over more CUs finishes sooner although X and the slabs are then read by
-// more blocks (the k16 order per output is the same for any count).  One
-// wave per block, which leaves a wave the whole slab to fetch, measured
-// slower for the 64-row GeGLU slabs and no faster elsewhere.
-inline int slab_waves(int64_t M, int64_t tiles_n, int cus) {
-  return tiles_n * ((M + 63) / 64) <= cus ? 2 : 4;
+// Waves per slab block (each takes 32 rows of X): two for slabs of at most
+// 32 x 768 weights when those blocks fit one per CU, else four.  A launch
+// spread over more CUs finishes sooner although X and the slabs are then read
+// by more blocks (the k16 order per output is the same for any count), as
+// long as a wave's share of the slab stays small: at two waves the 64-row
+// GeGLU slab and the K = 1152 slab measured slower, and one wave per block
+// (the whole slab to fetch) slower still.
+inline int slab_waves(int64_t M, int64_t tiles_n, int64_t slab_elems, int cus) {
+  return slab_elems <= 32 * 768 && tiles_n * ((M + 63) / 64) <= cus ? 2 : 4;
 }
 
 // Small-M launcher for 16-bit weights: slabs of 32 (GeGLU: 64) W rows, 64
@@ -1439,7 +1440,7 @@ void launch_slab_t(hipStream_t st, int cus, const uint16_t* x, int64_t ldx, cons
                    const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K, unsigned pan) {
   constexpr int TNO = GEGLU ? TN / 2 : TN;
   const int tiles_n = (N + 32 * TNO - 1) / (32 * TNO);
-  const int nw = slab_waves(M, tiles_n, cus), chunks = (M + 32 * nw - 1) / (32 * nw);
+  const int nw = slab_waves(M, tiles_n, (int64_t)32 * TN * K, cus), chunks = (M + 32 * nw - 1) / (32 * nw);
   const size_t lds = (size_t)32 * TN * K * sizeof(uint16_t);
   HB_REQUIRE(lds <= 160 * 1024, "hb_linear: weight slab too large for LDS");
   const int S = K / 16;
