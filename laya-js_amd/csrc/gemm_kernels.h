@@ -435,9 +435,17 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_mfma(const uint16_t* __restr
 // fragment read that share a row group hit 8 distinct bank groups.  Blocks
 // are numbered row-chunk-fastest and dealt to XCDs in contiguous runs: the
 // blocks that read one slab share an XCD's L2.
-template <int TN, int P, bool BF16, bool GEGLU>
+//
+// Quantized weights (QB = 8 or 4, f16 scales and zeros, groups a multiple of
+// 8): the slab's codes (its rows are contiguous runs of the code matrix) and
+// its scales and zeros go to LDS by direct-to-LDS loads beside the f16 slab,
+// and after the one wait every thread dequantizes its share of the slab's
+// 8-weight chunks into the f16 slab (dequant8, the other kernels' rounding),
+// so the MFMA steps and their bits are those of the 16-bit path.
+template <int TN, int P, bool BF16, bool GEGLU, int QB = 0, bool AFF = false>
 __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X, int64_t ldx,
-                                                 const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
+                                                 const uint16_t* __restrict__ W, QW qw,
+                                                 const uint16_t* __restrict__ bias,
                                                  const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
                                                  int64_t ldy, int M, int N, int K, int chunks, int xpan, int ypan) {
   constexpr int TNO = GEGLU ? TN / 2 : TN;  // output column blocks
@@ -476,21 +484,77 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
       rb[j][g] = bvec && col + 4 <= N ? *(const uint2v*)(bias + col) : uint2v{0, 0};
       rbg[j][g] = GEGLU && bvec && col + 4 <= N ? *(const uint2v*)(bias + N + col) : uint2v{0, 0};
     }
-  // the slab: DMA instruction q (of wave q % nw) fills block q, i.e. slab rows
-  // 8 * (q / KB) + lane / 8, k block q % KB; lane l fetches chunk (l%8) ^ (row%8)
-  const int nq = (SR / 8) * KB;
-  for (int q = wave; q < nq; q += nw) {
-    const int rb8 = q / KB, kb = q - rb8 * KB;
-    const int r = rb8 * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+  // slab row r -> W row (GeGLU: gate rows from SR / 2 on); rows past N are
+  // clamped, their outputs never stored
+  auto slab_wrow = [&](int r) -> int {
     const bool gate = GEGLU && r >= SR / 2;
     const int cc = n0 + (gate ? r - SR / 2 : r);
-    const int wrow = (cc < N ? cc : N - 1) + (gate ? N : 0);  // rows past N: clamped, never stored
-    __builtin_amdgcn_global_load_lds((const void*)(W + (int64_t)wrow * K + kb * 64 + c * 8),
-                                     (__attribute__((address_space(3))) void*)(smem + q * 512), 16, 0, 0);
+    return (cc < N ? cc : N - 1) + (gate ? N : 0);
+  };
+  const int nq = (SR / 8) * KB;
+  // quantized: codes [SR][K * QB / 8 bytes], then scales and zeros [SR][G],
+  // each f16 in the low half of a 32-bit slot (a 2-byte direct-to-LDS load
+  // writes lane l's value at 4 l), after the f16 slab
+  constexpr int CRB = QB ? 8 / QB : 1;  // weights per code byte (QB = 4: 2)
+  const int rowb = QB ? K / CRB : 0;     // code bytes per row
+  uint8_t* codes = (uint8_t*)(smem + SR * K);
+  uint32_t* szs = (uint32_t*)(codes + SR * rowb);
+  if constexpr (QB == 0) {
+    // the slab: DMA instruction q (of wave q % nw) fills block q, i.e. slab
+    // rows 8 * (q / KB) + lane / 8, k block q % KB; lane l fetches chunk
+    // (l%8) ^ (row%8)
+    for (int q = wave; q < nq; q += nw) {
+      const int rb8 = q / KB, kb = q - rb8 * KB;
+      const int r = rb8 * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+      __builtin_amdgcn_global_load_lds((const void*)(W + (int64_t)slab_wrow(r) * K + kb * 64 + c * 8),
+                                       (__attribute__((address_space(3))) void*)(smem + q * 512), 16, 0, 0);
+    }
+  } else {
+    // codes: instruction q fills bytes [1024 q, 1024 q + 1024) of the code
+    // block, 16 of one row per lane (rowb % 16 == 0)
+    const int ncq = SR * rowb / 1024;
+    for (int q = wave; q < ncq; q += nw) {
+      const int b = q * 1024 + lane * 16, r = b / rowb;
+      __builtin_amdgcn_global_load_lds((const void*)(qw.q + (int64_t)slab_wrow(r) * rowb + (b - r * rowb)),
+                                       (__attribute__((address_space(3))) void*)(codes + q * 1024), 16, 0, 0);
+    }
+    // scales (then zeros): 2 bytes per lane into 4-byte slots, instruction q
+    // entries [64 q, 64 q + 64) of the slab's [SR][G]
+    const int G = qw.G, nsq = (SR * G + 63) / 64;
+    for (int q = wave; q < (AFF ? 2 : 1) * nsq; q += nw) {
+      const bool zq = q >= nsq;
+      const int e = (zq ? q - nsq : q) * 64 + lane, r = e / G;
+      if (e < SR * G)
+        __builtin_amdgcn_global_load_lds(
+            (const void*)((const uint16_t*)(zq ? qw.zeros : qw.scales) + (int64_t)slab_wrow(r) * G + (e - r * G)),
+            (__attribute__((address_space(3))) void*)(szs + (zq ? SR * G : 0) + (q - (zq ? nsq : 0)) * 64), 2, 0,
+            0);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): everything above has landed
   __syncthreads();
-  if ((mc * nw + wave) * 32 >= M) return;  // a wave past the last row (after the barrier: its DMA share is done)
+  if constexpr (QB != 0) {
+    // dequantize: chunk i (8 weights) is slab row i / (K/8), chunk i % (K/8)
+    // of the row, into the f16 slab's layout
+    const int cpr = K >> 3, G = qw.G, nth = nw * 64;
+    for (int i = tid; i < SR * cpr; i += nth) {
+      const int r = i / cpr, c = i - r * cpr;
+      uint32_t w0, w1 = 0;
+      if constexpr (QB == 8) {
+        const uint2v w = *(const uint2v*)(codes + r * rowb + 8 * c);
+        w0 = w.x;
+        w1 = w.y;
+      } else {
+        w0 = *(const uint32_t*)(codes + r * rowb + 4 * c);
+      }
+      const int gi = r * G + (8 * c) / qw.group;
+      const uint32_t sb = szs[gi] & 0xffffu, zb = AFF ? szs[SR * G + gi] & 0xffffu : 0u;
+      *(uint4v*)(smem + ((r >> 3) * KB + (c >> 3)) * 512 + (r & 7) * 64 + (((c & 7) ^ (r & 7)) << 3)) =
+          dequant8<QB, AFF, false, BF16>(w0, w1, sb, zb, 0.f, 0.f);
+    }
+    __syncthreads();
+  }
+  if ((mc * nw + wave) * 32 >= M) return;  // a wave past the last row (after the barriers: its share is done)
 
   // W fragment of column block j, k16 step s (slab row 32 j + l32)
   auto wfrag = [&](int j, int s) __attribute__((always_inline)) -> uint4v {
@@ -1435,13 +1499,30 @@ inline int slab_waves(int64_t M, int64_t tiles_n, int64_t slab_elems, int cus) {
 // Small-M launcher for 16-bit weights: slabs of 32 (GeGLU: 64) W rows, 64
 // or 128 rows of X per block (slab_waves).  P (X steps held in registers)
 // is the largest of 48, 36, 32, 24, 16 and 4 that divides K/16.
-template <int TN, bool BF16, bool GEGLU>
-void launch_slab_t(hipStream_t st, int cus, const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias,
-                   const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K, unsigned pan) {
+// LDS bytes of a slab block: the f16 slab of 32 tn rows, and for quantized
+// weights the slab's codes and its scales (and zeros: aff), G per row in
+// 4-byte slots
+inline int64_t slab_lds(int64_t K, int tn, int qb, bool aff, int64_t G) {
+  const int64_t sr = 32 * tn;
+  return sr * K * 2 + (qb ? sr * K * qb / 8 + sr * G * 4 * (aff ? 2 : 1) : 0);
+}
+
+// Quantized weights on the slab kernel: f16 scales, groups a multiple of 8
+// (a chunk of 8 weights in one group), K / 16 a multiple of 48 or 36 (the
+// register depths instantiated for them), and the block's LDS within bounds.
+inline bool qslab_ok(int64_t K, int tn, int qb, bool aff, const QW& qw) {
+  return qw.group % 8 == 0 && ((K / 16) % 48 == 0 || (K / 16) % 36 == 0) &&
+         slab_lds(K, tn, qb, aff, qw.G) <= 160 * 1024;
+}
+
+template <int TN, bool BF16, bool GEGLU, int QB = 0, bool AFF = false>
+void launch_slab_t(hipStream_t st, int cus, QW qw, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                   const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N,
+                   int K, unsigned pan) {
   constexpr int TNO = GEGLU ? TN / 2 : TN;
   const int tiles_n = (N + 32 * TNO - 1) / (32 * TNO);
   const int nw = slab_waves(M, tiles_n, (int64_t)32 * TN * K, cus), chunks = (M + 32 * nw - 1) / (32 * nw);
-  const size_t lds = (size_t)32 * TN * K * sizeof(uint16_t);
+  const int64_t lds = slab_lds(K, TN, QB, AFF, QB ? qw.G : 0);
   HB_REQUIRE(lds <= 160 * 1024, "hb_linear: weight slab too large for LDS");
   const int S = K / 16;
   auto go = [&](auto kern) {
@@ -1449,15 +1530,21 @@ void launch_slab_t(hipStream_t st, int cus, const uint16_t* x, int64_t ldx, cons
     once_per_device(attr, [&] {
       HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     });
-    kern<<<tiles_n * chunks, 64 * nw, lds, st>>>(x, ldx, w, bias, r, ldr, y, ldy, M, N, K, chunks,
-                                              (pan & HB_X_PANEL) ? 1 : 0, (pan & HB_Y_PANEL) ? 1 : 0);
+    kern<<<tiles_n * chunks, 64 * nw, (size_t)lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, chunks,
+                                                          (pan & HB_X_PANEL) ? 1 : 0, (pan & HB_Y_PANEL) ? 1 : 0);
   };
-  if (S % 48 == 0) go(gemm_slab<TN, 48, BF16, GEGLU>);
-  else if (S % 36 == 0) go(gemm_slab<TN, 36, BF16, GEGLU>);
-  else if (S % 32 == 0) go(gemm_slab<TN, 32, BF16, GEGLU>);
-  else if (S % 24 == 0) go(gemm_slab<TN, 24, BF16, GEGLU>);
-  else if (S % 16 == 0) go(gemm_slab<TN, 16, BF16, GEGLU>);
-  else go(gemm_slab<TN, 4, BF16, GEGLU>);
+  if constexpr (QB != 0) {
+    HB_REQUIRE(S % 48 == 0 || S % 36 == 0, "hb_linear: quantized slab needs K a multiple of 768 or 576");
+    if (S % 48 == 0) go(gemm_slab<TN, 48, BF16, GEGLU, QB, AFF>);
+    else go(gemm_slab<TN, 36, BF16, GEGLU, QB, AFF>);
+  } else {
+    if (S % 48 == 0) go(gemm_slab<TN, 48, BF16, GEGLU>);
+    else if (S % 36 == 0) go(gemm_slab<TN, 36, BF16, GEGLU>);
+    else if (S % 32 == 0) go(gemm_slab<TN, 32, BF16, GEGLU>);
+    else if (S % 24 == 0) go(gemm_slab<TN, 24, BF16, GEGLU>);
+    else if (S % 16 == 0) go(gemm_slab<TN, 16, BF16, GEGLU>);
+    else go(gemm_slab<TN, 4, BF16, GEGLU>);
+  }
 }
 
 // The slab kernel pays off while its blocks fit one per CU: its X fragment
@@ -1489,9 +1576,10 @@ void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int
   else if (arow_path(M))
     launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   else {
-    if constexpr (QB == 0) {
-      if (slab_path(M, N, K, GEGLU, cus)) {
-        launch_slab_t<GEGLU ? 2 : 1, BF16, GEGLU>(st, cus, x, ldx, w, bias, r, ldr, y, ldy, M, N, K, pan);
+    if constexpr (QB == 0 || !SF32) {
+      if (slab_path(M, N, K, GEGLU, cus) && (QB == 0 || qslab_ok(K, GEGLU ? 2 : 1, QB, AFF, qw))) {
+        launch_slab_t<GEGLU ? 2 : 1, BF16, GEGLU, QB, AFF>(st, cus, qw, x, ldx, w, bias, r, ldr, y, ldy, M, N, K,
+                                                          pan);
         return;
       }
     }

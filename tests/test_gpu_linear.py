@@ -188,6 +188,52 @@ def test_qlinear_bf16(b, M, bits):
     b.dispose(X)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_quantized_small_m_slab_bits_equal_large_m(b, dtype):
+    """Quantized weights on the small-M slab kernel (the slab's codes, scales
+    and zeros fetched to LDS and dequantized once into the f16 slab): against
+    the oracle's dequantize-then-linear (max-rel <= 1e-2), and bit for bit
+    against the same rows inside a 4096-row input, which the large-M kernel
+    computes with the same dequantization and k16 order.  Shapes: attn Wo and
+    mlp Wo (K = 1152) with residuals, Wi + GeGLU, a ragged output width with
+    K = 576; q8 symmetric and q4 affine; groups of 64 and 32."""
+    from laya_hip import compose as C
+    rng = np.random.default_rng(41)
+    cases = [(128, 768, 768, False, 8, 64, True), (512, 768, 1152, False, 4, 64, True),
+             (77, 2304, 768, True, 4, 32, False), (200, 784, 576, False, 8, 32, False)]
+    for (M, N2, K, geglu, bits, g, resid) in cases:
+        print(f"quantized slab M={M} N={N2} K={K} geglu={geglu} q{bits} g{g} resid={resid} {dtype}", flush=True)
+        h, q, sf, zf = _quantized(rng, N2, K, bits, g)
+        Q = C.upload_quantized(b, h, dtype)
+        assert Q.native
+        N = N2 // 2 if geglu else N2
+        x = rounded(rng.standard_normal((M, K)), dtype)
+        r = rounded(rng.standard_normal((M, N)), dtype)
+
+        def run(xs, rs):
+            X, R = b.fromHost(to_host(xs, dtype)), b.fromHost(to_host(rs, dtype))
+            y = C.quantized_linear(b, X, Q)
+            y = b.geglu(y) if geglu else y
+            y = b.add(R, y) if resid else y
+            out = np.asarray(b.read(y).data)
+            got = read32(b, y)
+            for t in (X, R, y):
+                b.dispose(t)
+            return out, got
+
+        out, got = run(x, r)
+        lin = cr.quantized_linear(x, q, sf, zf, g, dtype=dtype)
+        ref = cr.geglu(rounded(lin, dtype)) if geglu else lin
+        ref = r + rounded(ref, dtype) if resid else ref
+        err = max_rel(got, ref)
+        assert err <= 1e-2, f"M={M} N={N2} K={K} q{bits}: max-rel {err:.2e}"
+        xb = np.concatenate([x, rounded(rng.standard_normal((4096 - M, K)), dtype)])
+        rb = np.concatenate([r, rounded(rng.standard_normal((4096 - M, N)), dtype)])
+        big, _ = run(xb, rb)
+        np.testing.assert_array_equal(out, big[:M])
+        C.dispose_quantized(b, Q)
+
+
 @pytest.mark.parametrize("bits,mode", [(8, "symmetric"), (4, "affine"), (8, "affine"), (4, "symmetric")])
 def test_qlinear_one_hot_reads_exact_weights(b, bits, mode):
     """x = identity rows: y[k, n] = dequant(W)[n, k] must equal fl16(q*s + z)
