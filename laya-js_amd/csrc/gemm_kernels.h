@@ -1565,17 +1565,24 @@ template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
 void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
                           QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
                           int N, int K) {
-  // large M: persistent 256 x 192 tiles with register-resident A rows; small
-  // M: weight-stationary slabs (16-bit weights), else 128 x 128 tiles.  The
-  // large-M variant without a K tail takes quantized weights in groups of 64
-  // (one scale per row and stage) whose scale table it can address with
-  // 32-bit offsets; other groups take the general one.
-  const bool whole = K % 64 == 0 && (QB == 0 || (qw.group == 64 && (int64_t)(GEGLU ? 2 * N : N) * qw.G * 2 < 0x7ffffff0));
-  if (arow_path(M) && whole)
-    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, false>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-  else if (arow_path(M))
-    launch_arow<192, BF16, GEGLU, QB, AFF, SF32, true>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-  else {
+  // large M: persistent 256 x 192 tiles with register-resident A rows (16-bit
+  // weights: hb_qlinear dequantizes a quantized weight once and calls the
+  // 16-bit path at large M); small M: weight-stationary slabs, else 128 x 128
+  // tiles.  K % 64 != 0 takes the large-M variant with a K tail.
+  if constexpr (QB == 0) {
+    if (arow_path(M)) {
+      if (K % 64 == 0)
+        launch_arow<192, BF16, GEGLU, 0, false, false, false>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M,
+                                                              N, K);
+      else
+        launch_arow<192, BF16, GEGLU, 0, false, false, true>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N,
+                                                             K);
+      return;
+    }
+  } else {
+    HB_REQUIRE(!arow_path(M), "hb_qlinear: large-M quantized weights are dequantized before the GEMM");
+  }
+  {
     if constexpr (QB == 0 || !SF32) {
       if (slab_path(M, N, K, GEGLU, cus) && (QB == 0 || qslab_ok(K, GEGLU ? 2 : 1, QB, AFF, qw))) {
         launch_slab_t<GEGLU ? 2 : 1, BF16, GEGLU, QB, AFF>(st, cus, qw, x, ldx, w, bias, r, ldr, y, ldy, M, N, K,
