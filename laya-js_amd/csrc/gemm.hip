@@ -2,7 +2,7 @@
 // 16-bit weights and for laya's quantized weight format (q8 / q4 with
 // per-group scales and zeros).
 //
-// Two MFMA kernels, both on gfx950's v_mfma_f32_32x32x16_{f16,bf16} with the
+// Three MFMA kernels, all on gfx950's v_mfma_f32_32x32x16_{f16,bf16} with the
 // same operand order (W rows as the A operand, X rows as the B operand) and
 // the same sequence of k16 steps, so a row's output bits do not depend on M:
 // - gemm_mfma_arow (M >= 4096): persistent, 256 x 192 tiles, one wave per
@@ -11,17 +11,20 @@
 //   same LDS C tile) is staged in LDS and written during the first stages of
 //   the block's next tile.  X and Y may be row-major or in panel order
 //   (32-row x 16-column blocks of 1 KB laid out as MFMA operands);
-// - gemm_mfma (smaller M): 128 x 128 tiles, A and B double-buffered in LDS,
-//   epilogue staged in LDS and written with 16-byte stores.
-// Both take 64-wide K stages of 16-byte chunks XOR-swizzled by row so the
+// - gemm_slab (small M, K % 64 == 0): weight-stationary, the whole W slab of
+//   a block in LDS, every X fragment in registers, one wait for memory;
+// - gemm_mfma (the rest below M = 4096): 128 x 128 tiles, A and B
+//   double-buffered in LDS, epilogue staged in LDS, 16-byte stores.
+// W tiles are 64-wide K stages of 16-byte chunks XOR-swizzled by row so the
 // fragment reads of consecutive rows spread over the LDS banks.  The
 // epilogue adds the bias, rounds once to the storage type, applies GeGLU on
 // (value, gate) column pairs held by the same lane, and adds the residual
-// (y = round(round(x.w^T + b) + r), the linear-then-add order).  For
-// quantized weights the W loader fetches the packed codes (8 or 4 bytes per
-// 8 weights) and the group's scale / zero, dequantizes them in registers to
-// fl16(q*s + z) -- one correctly rounded f16 fma, the value host
-// dequantization would upload -- and stages f16 into LDS for the same MFMA.
+// (y = round(round(x.w^T + b) + r), the linear-then-add order).  Quantized
+// weights are dequantized to fl16(q*s + z) -- one correctly rounded f16 fma,
+// the value host dequantization would upload -- by one routine (dequant8):
+// in the 128 x 128 kernel's W loader, into the slab in LDS, and at
+// M >= 4096 once per call into a pooled 16-bit copy that the 16-bit large-M
+// kernel then reads (dequant_rows_kernel).
 // Blocks walk the tile grid in an XCD-aware order: the hardware deals block b
 // to XCD b % 8, so each XCD is given a contiguous run of row panels (their A
 // rows and the whole W stay in that XCD's L2).

@@ -658,12 +658,12 @@ __global__ __launch_bounds__(256) void gemm_slab(const uint16_t* __restrict__ X,
 // of column blocks whose lanes hold the rotation partners d and d + 32 at the
 // same register, so RoPE is applied in registers, and the tile leaves
 // head-major.
-template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL, bool QKV = false>
+template <int BN, bool BF16, bool GEGLU, bool KTAIL, bool QKV = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_mfma_arow(
-    const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W, QW qw,
-    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y,
-    int64_t ldy, int M, int N, int K, int tiles_n, int tiles, int xpan, int ypan, QK qk) {
-  static_assert(!QKV || (!GEGLU && QB == 0 && BN % 64 == 0), "QKV: 16-bit weights, whole heads per tile");
+    const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
+    const uint16_t* __restrict__ R, int64_t ldr, uint16_t* __restrict__ Y, int64_t ldy, int M, int N, int K,
+    int tiles_n, int tiles, int xpan, int ypan, QK qk) {
+  static_assert(!QKV || (!GEGLU && BN % 64 == 0), "QKV: no GeGLU, whole heads per tile");
   constexpr int NT = 256, BM = 256, BK = 64;
   constexpr int TM = 2, TN = BN / 32;  // 32x32 blocks per wave
   constexpr int KS = BK / 16;          // k16 substeps per stage
@@ -678,15 +678,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* Bs = smem;               // [2][BN*64] W tiles
   uint16_t* Cs = smem + 2 * BN * BK;  // [RG][BM][8] 16-byte chunks: residual in, output out
-  // Quantized weights in whole groups of 64 (the variant without a K tail;
-  // the launcher sends other group sizes to the one with): the scale (and
-  // zero) of a W tile row for a stage is loaded once, three stages ahead, by
-  // the thread of that number, and reaches the eight threads that
-  // dequantize the row through Zs, two stages of one 32-bit entry
-  // (s | z << 16) per thread.  Every chunk loaded its own copy before.
-  constexpr bool QRING = QB != 0 && !KTAIL;
-  static_assert(!QRING || !SF32, "quantized large-M path: f16 scales and zeros");
-  uint32_t* Zs = (uint32_t*)(Cs + RG * BM * 64);  // [2][NT]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lg = lane >> 5;
@@ -762,29 +753,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   struct BRegs {
     uint4v v[B_LD];
-    uint32_t s[QB && !QRING ? B_LD : 1], z[QB && !QRING ? B_LD : 1];
-    float sf[QB && SF32 ? B_LD : 1], zf[QB && SF32 ? B_LD : 1];
   };
   // B tile row r -> W row (GEGLU: first half value rows, second half gate
-  // rows).  wlane: byte offsets of the lane's W pieces from the tile's first
-  // row of their half (16-bit weights: 16 bytes per 8 values; quantized: QB
-  // bytes of codes); load i holds rows 32i + tid/8, gate rows from
-  // i = B_LD / 2 on.
+  // rows).  wlane: byte offsets of the lane's 16-byte W pieces from the
+  // tile's first row of their half; load i holds rows 32i + tid/8, gate rows
+  // from i = B_LD / 2 on.
   static_assert(!GEGLU || (B_LD % 2 == 0 && (B_LD / 2) * (NT / 8) == BN / 2), "GEGLU halves of the W loads");
-  constexpr int WCB = QB ? QB : 16;  // bytes per 8 weights
-  const int64_t wrow_b = (int64_t)K * WCB / 8;  // bytes per W row
+  const int64_t wrow_b = (int64_t)K * 2;  // bytes per W row
   uint32_t wlane[B_LD];
 #pragma unroll
   for (int i = 0; i < B_LD; i++) {
     const int q = tid + i * NT, r = q >> 3, c = q & 7;
     const int rr = GEGLU && r >= BN / 2 ? r - BN / 2 : r;
-    wlane[i] = (uint32_t)(rr * wrow_b + c * WCB);
+    wlane[i] = (uint32_t)(rr * wrow_b + c * 16);
   }
   auto load_b = [&](int n0, int k0, BRegs& br) {
     if constexpr (BUFW) {
       // value rows from W row n0, gate rows (GEGLU) from W row N + n0; each
       // resource ends with row N - 1 of its half
-      const uint8_t* wb = QB ? qw.q : (const uint8_t*)W;
+      const uint8_t* wb = (const uint8_t*)W;
       const int64_t left = (int64_t)(N - n0) * wrow_b;
       const int nrec = (int)(left < 0x7ffffff0 ? left : 0x7ffffff0);
       const __amdgpu_buffer_rsrc_t rv =
@@ -794,14 +781,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int i = 0; i < B_LD; i++) {
         const __amdgpu_buffer_rsrc_t rs = GEGLU && i >= B_LD / 2 ? rg : rv;
-        if constexpr (QB == 8) {
-          const uint2v c = __builtin_bit_cast(uint2v, __builtin_amdgcn_raw_buffer_load_b64(rs, wlane[i], k0, 0));
-          br.v[i] = uint4v{c.x, c.y, 0, 0};
-        } else if constexpr (QB == 4) {
-          br.v[i] = uint4v{__builtin_amdgcn_raw_buffer_load_b32(rs, wlane[i], k0 / 2, 0), 0, 0, 0};
-        } else {
-          br.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, wlane[i], k0 * 2, 0);
-        }
+        br.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, wlane[i], k0 * 2, 0);
       }
       return;
     }
@@ -812,40 +792,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int nn = GEGLU ? n0 + (r < BN / 2 ? r : r - BN / 2) : n0 + r;
       const bool rv = nn < N;
       const int wr = GEGLU && r >= BN / 2 ? N + nn : nn;
-      if constexpr (QB == 0) {
-        const uint4v v = *(const uint4v*)(W + (int64_t)(rv ? wr : 0) * K + (KTAIL && k >= K ? 0 : k));
-        br.v[i] = (KTAIL && k >= K) ? uint4v{0, 0, 0, 0} : v;
-      } else {
-        br.v[i] = uint4v{0, 0, 0, 0};
-        br.s[i] = br.z[i] = 0;
-        if constexpr (SF32) br.sf[i] = br.zf[i] = 0.f;
-        if (rv && k < K) {
-          const int64_t row = wr;
-          if constexpr (QB == 8) {
-            uint2v w = *(const uint2v*)(qw.q + row * K + k);
-            br.v[i].x = w.x;
-            br.v[i].y = w.y;
-          } else {
-            br.v[i].x = *(const uint32_t*)(qw.q + row * (K / 2) + k / 2);
-          }
-          const int64_t gi = row * qw.G + k / qw.group;
-          if constexpr (SF32) {
-            br.sf[i] = ((const float*)qw.scales)[gi];
-            if constexpr (AFF) br.zf[i] = ((const float*)qw.zeros)[gi];
-          } else {
-            br.s[i] = ((const uint16_t*)qw.scales)[gi];
-            if constexpr (AFF) br.z[i] = ((const uint16_t*)qw.zeros)[gi];
-          }
-        }
-      }
-    }
-  };
-  // scales of the stage's W rows, read from the ring ahead of store_b
-  uint32_t szv[B_LD];
-  auto read_sz = [&](int buf) __attribute__((always_inline)) {
-    if constexpr (QRING) {
-#pragma unroll
-      for (int i = 0; i < B_LD; i++) szv[i] = Zs[buf * NT + ((tid + i * NT) >> 3)];
+      const uint4v v = *(const uint4v*)(W + (int64_t)(rv ? wr : 0) * K + (KTAIL && k >= K ? 0 : k));
+      br.v[i] = (KTAIL && k >= K) ? uint4v{0, 0, 0, 0} : v;
     }
   };
   auto store_b = [&](int buf, const BRegs& br) {
@@ -853,47 +801,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int i = 0; i < B_LD; i++) {
       int q = tid + i * NT, r = q >> 3, c = q & 7;
-      if constexpr (QB == 0) {
-        *(uint4v*)(b + swz(r, c)) = br.v[i];
-      } else if constexpr (QRING) {
-        const uint32_t sz = szv[i];  // from the stage's ring slot (its W buffer)
-        *(uint4v*)(b + swz(r, c)) = dequant8<QB, AFF, false, BF16>(br.v[i].x, br.v[i].y, sz & 0xffffu, sz >> 16,
-                                                                    0.f, 0.f);
-      } else {
-        float sf = 0.f, zf = 0.f;
-        if constexpr (SF32) {
-          sf = br.sf[i];
-          zf = br.zf[i];
-        }
-        *(uint4v*)(b + swz(r, c)) = dequant8<QB, AFF, SF32, BF16>(br.v[i].x, br.v[i].y, br.s[i], br.z[i], sf, zf);
-      }
+      *(uint4v*)(b + swz(r, c)) = br.v[i];
     }
   };
-  // The scale and zero of W tile row tid (threads past BN repeat the last
-  // row) for the stage at k0 of the tile at n0: scales / zeros are f16
-  // [rows, G] with one group per stage.
-  const int64_t sz_bytes = (int64_t)(GEGLU ? 2 * N : N) * qw.G * 2;
-  const int sz_rec = (int)(sz_bytes < 0x7ffffff0 ? sz_bytes : 0x7ffffff0);
-  auto load_sz = [&](int n0, int k0) __attribute__((always_inline)) -> uint32_t {
-    if constexpr (QRING) {
-      int t = tid < BN ? tid : BN - 1;
-      asm volatile("" : "+v"(t));  // per-stage address math, not hoisted
-      const int wrow = GEGLU && t >= BN / 2 ? N + n0 + t - BN / 2 : n0 + t;
-      const uint32_t voff = (uint32_t)wrow * (uint32_t)qw.G * 2u;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)qw.scales, (short)0, sz_rec, BUF_FLAGS);
-      const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, k0 >> 5, 0);
-      if constexpr (AFF) {
-        const __amdgpu_buffer_rsrc_t rz =
-            __builtin_amdgcn_make_buffer_rsrc((void*)qw.zeros, (short)0, sz_rec, BUF_FLAGS);
-        return sv | ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, voff, k0 >> 5, 0) << 16);
-      }
-      return sv;
-    }
-    return 0;
-  };
-  uint32_t zr[2] = {0, 0};  // scales of the stage two ahead (zr[g & 1] at step g), and three ahead
-  constexpr int NZ = QRING ? (AFF ? 2 : 1) : 0;  // their loads per stage
 
   // column block j of the tile -> W tile row (GEGLU: value blocks, then gate blocks)
   auto bcol = [&](int j) -> int {
@@ -1263,16 +1173,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int k2b = __builtin_amdgcn_readfirstlane(wrap ? nxt_kb + (k2 - KT) * nxt_ks : k2 * BK);
     load_a(m2, k2b, al);
     load_b(n2, k2b, bl);
-    if constexpr (QRING) {
-      // the scales of stage g + 3 (the step's position SP has the parity of g)
-      const int k3 = __builtin_amdgcn_readfirstlane(kin + 3);
-      const int wrap3 = __builtin_amdgcn_readfirstlane(k3 >= KT ? 1 : 0);
-      const int n3 = __builtin_amdgcn_readfirstlane(wrap3 ? nxt_n0 : cur_n0);
-      const int k3b = __builtin_amdgcn_readfirstlane(wrap3 ? nxt_kb + (k3 - KT) * nxt_ks : k3 * BK);
-      zr[(SP + 1) & 1] = load_sz(n3, k3b);
-    }
     const uint16_t* b = Bs + (g & 1) * BN * BK;
-    read_sz((g + 1) & 1);
     uint4v bf[KS][TN];
 #pragma unroll
     for (int s = 0; s < KS; s++)
@@ -1289,9 +1190,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // one global load (while any remain) and one fragment read of the next
     // substep; the write-out's C-tile reads ride with the last loads, its
     // stores follow every load; the W staging for the next stage goes last
-    constexpr int NVMEM = TM * KS + B_LD + NZ, NPAIR = KS * TN, WOS = WO ? WO_PS : 0;
+    constexpr int NVMEM = TM * KS + B_LD, NPAIR = KS * TN, WOS = WO ? WO_PS : 0;
     static_assert(NVMEM + 2 + WOS <= NPAIR, "write-out stores after the loads");
-    __builtin_amdgcn_sched_group_barrier(0x100, TN + (QRING ? B_LD : 0), 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
 #pragma unroll
     for (int p = 0; p < NPAIR; p++) {
       if (p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
@@ -1301,9 +1202,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
     }
     store_b((g + 1) & 1, bs);
-    // the scales of stage g + 2 into its ring slot, read by the next step
-    if constexpr (QRING) Zs[(g & 1) * NT + tid] = zr[SP & 1];
-    __builtin_amdgcn_sched_group_barrier(0x200, B_LD + (QRING ? 1 : 0), 0);
+    __builtin_amdgcn_sched_group_barrier(0x200, B_LD, 0);
     // the residual tile arrives in the C tile while the tile computes: piece
     // p at stage dma0 + min(p, dpl), the last ones together
     if (R != nullptr && kin - SP == dma0 && SP <= dpl) {
@@ -1324,16 +1223,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int g1 = S > 1 ? 1 : 0, i1 = g1 / KT, k1 = (g1 - i1 * KT) * BK;
     load_a(m0, 0, A0);
     load_b(n0, 0, B0);
-    if constexpr (QRING) {
-      // the scales of stages 0 and 1 into the ring, those of stage 2 held
-      const int g2 = S > 2 ? 2 : S - 1, i2 = g2 / KT, k2 = (g2 - i2 * KT) * BK;
-      const uint32_t z0 = load_sz(n0, 0), z1 = load_sz(tile_n0(i1), k1);
-      zr[0] = load_sz(tile_n0(i2), k2);
-      Zs[tid] = z0;
-      Zs[NT + tid] = z1;
-      __syncthreads();
-      read_sz(0);
-    }
     store_b(0, B0);
     load_a(tile_m0(i1), k1, A1);
     load_b(tile_n0(i1), k1, B1);
@@ -1405,7 +1294,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // barrier makes every wave's part of the C tile visible (and, without R,
     // keeps the previous tile's write-out reads ahead of this epilogue's
     // writes).
-    constexpr int VM1 = TM * KS + B_LD + NZ;  // the loads of one stage (stages after the pieces store nothing)
+    constexpr int VM1 = TM * KS + B_LD;  // the loads of one stage (stages after the pieces store nothing)
     static_assert(VM1 <= 63, "vmcnt immediate");
     if (R != nullptr) {
       if (dma0 + dpl >= KT - 1) __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -1461,10 +1350,10 @@ void launch_mfma(hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t*
   kern<<<tiles_m * tiles_n, WM * WN * 64, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n);
 }
 
-template <int BN, bool BF16, bool GEGLU, int QB, bool AFF, bool SF32, bool KTAIL, bool QKV = false>
+template <int BN, bool BF16, bool GEGLU, bool KTAIL, bool QKV = false>
 void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
-                        QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
-                        int N, int K, QK qk = QK{nullptr, 1, 1}) {
+                 const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M, int N, int K,
+                 QK qk = QK{nullptr, 1, 1}) {
   constexpr int BNO = GEGLU ? BN / 2 : BN;
   const int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO, tiles = tiles_m * tiles_n;
   // one persistent block per CU, a multiple of 8 (one per XCD); with
@@ -1474,14 +1363,14 @@ void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64
   int grid = KT % 6 == 0 ? (tiles < cus ? tiles : cus) / 8 * 8 : 8 * (((tiles_m + 7) / 8) * tiles_n);
   HB_REQUIRE(grid >= 8, "hb_linear: large-M GEMM needs at least 8 tiles");
   constexpr int RG = (BNO / 8 + 7) / 8;
-  // W tiles, C tile, and for quantized weights the scale ring
-  const size_t lds = ((size_t)2 * BN * 64 + (size_t)RG * 256 * 64) * sizeof(uint16_t) + (QB ? 2 * 256 * 4 : 0);
-  auto kern = gemm_mfma_arow<BN, BF16, GEGLU, QB, AFF, SF32, KTAIL, QKV>;
+  // W tiles and the C tile
+  const size_t lds = ((size_t)2 * BN * 64 + (size_t)RG * 256 * 64) * sizeof(uint16_t);
+  auto kern = gemm_mfma_arow<BN, BF16, GEGLU, KTAIL, QKV>;
   static std::atomic<uint64_t> attr{0};
   once_per_device(attr, [&] {
     HB_CHECK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   });
-  kern<<<grid, 256, lds, st>>>(x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K, tiles_n, tiles, (pan & HB_X_PANEL) ? 1 : 0,
+  kern<<<grid, 256, lds, st>>>(x, ldx, w, bias, r, ldr, y, ldy, M, N, K, tiles_n, tiles, (pan & HB_X_PANEL) ? 1 : 0,
                                (pan & HB_Y_PANEL) ? 1 : 0, qk);
 }
 
@@ -1572,11 +1461,9 @@ void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int
   if constexpr (QB == 0) {
     if (arow_path(M)) {
       if (K % 64 == 0)
-        launch_arow<192, BF16, GEGLU, 0, false, false, false>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M,
-                                                              N, K);
+        launch_arow<192, BF16, GEGLU, false>(st, cus, pan, x, ldx, w, bias, r, ldr, y, ldy, M, N, K);
       else
-        launch_arow<192, BF16, GEGLU, 0, false, false, true>(st, cus, pan, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N,
-                                                             K);
+        launch_arow<192, BF16, GEGLU, true>(st, cus, pan, x, ldx, w, bias, r, ldr, y, ldy, M, N, K);
       return;
     }
   } else {
@@ -1613,8 +1500,7 @@ void mfma_dtype(int dt, bool geglu, hipStream_t st, int cus, unsigned pan, const
 template <bool BF16>
 void launch_qkv(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
                 uint16_t* y, int M, int N, int K, QK qk) {
-  launch_arow<192, BF16, false, 0, false, false, false, true>(st, cus, pan, x, ldx, w, QW{}, nullptr, nullptr, 0, y,
-                                                              0, M, N, K, qk);
+  launch_arow<192, BF16, false, false, true>(st, cus, pan, x, ldx, w, nullptr, nullptr, 0, y, 0, M, N, K, qk);
 }
 
 // Instantiated by gemm_f16.hip (QB = 0), gemm_q8.hip and gemm_q4.hip.
