@@ -111,6 +111,49 @@ def test_recorded_encoder_replays(b, B, T):
     enc.dispose()
 
 
+def test_recorded_quantized_linear_replays(b):
+    """A quantized linear at M = 4096 rows (its weight dequantized once per
+    call into a 16-bit copy from the pool, then the large-M GEMM), recorded
+    and replayed: every replay gives the eager bits, also after x is
+    rewritten in place; the copy's block stays with the graph and returns to
+    the pool when the graph is destroyed."""
+    from laya_hip import compose as C
+    from laya_hip.host import HostQuantized, pack_quantized
+    from oracle import cpu_ref as cr
+    rng = np.random.default_rng(9)
+    N, K, M = 768, 768, 4096
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    q, s, z = cr.quantize_matrix(w, N, K, 4, 64, refine=False)
+    h = HostQuantized((N, K), 4, 64, "affine", pack_quantized(q, 4), HostTensor("f16", s.shape, s.view(np.float16)),
+                      HostTensor("f16", z.shape, z.view(np.float16)))
+    Q = C.upload_quantized(b, h, "f16")
+    X = b.fromHost(HostTensor("f16", (M, K), rng.standard_normal((M, K)).astype(np.float16)))
+
+    def eager():
+        y = C.quantized_linear(b, X, Q)
+        out = _bits(b, y)
+        b.dispose(y)
+        return out
+
+    want = eager()
+    blocks0 = b.pool_stats()["live_blocks"]
+    g = b.capture(lambda: C.quantized_linear(b, X, Q))
+    for _ in range(3):
+        np.testing.assert_array_equal(_bits(b, g.run()), want)
+        np.testing.assert_array_equal(eager(), want)  # eager work between replays
+    b.write(X, HostTensor("f16", (M, K), rng.standard_normal((M, K)).astype(np.float16)))
+    got2 = _bits(b, g.run())
+    want2 = eager()
+    np.testing.assert_array_equal(got2, want2)
+    assert not np.array_equal(want2, want)
+    out = g.out
+    g.destroy()
+    b.dispose(out)
+    assert b.pool_stats()["live_blocks"] == blocks0
+    C.dispose_quantized(b, Q)
+    b.dispose(X)
+
+
 def test_recording_refuses_synchronizing_calls(b):
     """A read inside a recording is refused with a clear error (the host-side
     check runs before the stream is touched); the recording is dropped and
