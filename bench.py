@@ -489,7 +489,7 @@ def run_gemm_sweep(args) -> None:
         for M in (128, 512, 2048, 8192, 16384):
             X = be.fromHost(HostTensor("f16", (M, K), rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)))
             kinds = [("f16", lambda: be.linear(X, Wt))]
-            if M in (512, 8192):
+            if M in (512, 2048, 8192):
                 kinds += [(f"q{b}", (lambda b=b: C.quantized_linear(be, X, quants[b]))) for b in (8, 4)]
             for kind, fn in kinds:
                 def launch():

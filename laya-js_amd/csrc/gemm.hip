@@ -22,9 +22,9 @@
 // (y = round(round(x.w^T + b) + r), the linear-then-add order).  Quantized
 // weights are dequantized to fl16(q*s + z) -- one correctly rounded f16 fma,
 // the value host dequantization would upload -- by one routine (dequant8):
-// in the 128 x 128 kernel's W loader, into the slab in LDS, and at
-// M >= 4096 once per call into a pooled 16-bit copy that the 16-bit large-M
-// kernel then reads (dequant_rows_kernel).
+// in the 128 x 128 kernel's W loader, into the slab in LDS, and from
+// M = 1024 on (unless the slab kernel takes the call) once per call into a
+// pooled 16-bit copy that the 16-bit kernels then read (dequant_rows_kernel).
 // Blocks walk the tile grid in an XCD-aware order: the hardware deals block b
 // to XCD b % 8, so each XCD is given a contiguous run of row panels (their A
 // rows and the whole W stay in that XCD's L2).
@@ -321,11 +321,14 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
     const uint16_t* Rp = (const uint16_t*)r;
     uint16_t* Yp = (uint16_t*)y;
     int m = (int)M, n = (int)N, k = (int)K;
-    if (arow_path(M)) {
-      // Large M: the weight is dequantized once into a pooled 16-bit copy
-      // and the 16-bit GEMM runs on it (a loader that dequantizes repeats the
-      // work for every row tile: 22-34% over 16-bit weights, against one
-      // bandwidth-bound pass over the weight here)
+    const int cus0 = cu_count(ctx);
+    const bool slab = slab_path(M, N, K, geglu, cus0) && qslab_ok(K, geglu ? 2 : 1, bits, mode == 1, q);
+    if (arow_path(M) || (M >= 1024 && !slab)) {
+      // From M = 1024 (unless the slab kernel takes the call): the weight is
+      // dequantized once into a pooled 16-bit copy and the 16-bit GEMM runs
+      // on it.  A loader that dequantizes repeats the work for every row
+      // tile (at M = 8192: 22-34% over 16-bit weights, against one
+      // bandwidth-bound pass over the weight here).
       const int64_t rows = geglu ? 2 * N : N;
       uint16_t* wd = (uint16_t*)pool_alloc(ctx, (size_t)(rows * K * 2));
       const int cus = cu_count(ctx);
