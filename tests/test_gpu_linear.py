@@ -138,7 +138,7 @@ def _quantized(rng, N, K, bits, g=64):
 
 @pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("name", list(SHAPES))
-@pytest.mark.parametrize("M", [512, 8192])
+@pytest.mark.parametrize("M", [512, 2048, 8192])
 def test_qlinear_config2(b, name, M, bits):
     from laya_hip import compose as C
     N, K = SHAPES[name]
