@@ -330,7 +330,12 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
       // tile (at M = 8192: 22-34% over 16-bit weights, against one
       // bandwidth-bound pass over the weight here).
       const int64_t rows = geglu ? 2 * N : N;
-      uint16_t* wd = (uint16_t*)pool_alloc(ctx, (size_t)(rows * K * 2));
+      struct PoolBlock {  // back to the pool when the call ends, by return or throw
+        uintptr_t ctx;
+        void* p;
+        ~PoolBlock() { pool_free(ctx, p); }  // stream-ordered: reused only by work enqueued later
+      } held{ctx, pool_alloc(ctx, (size_t)(rows * K * 2))};
+      uint16_t* wd = (uint16_t*)held.p;
       const int cus = cu_count(ctx);
       if (bits == 8 && mode == 0) launch_dequant_rows<8, false>(st, cus, dt, q, wd, rows, k);
       else if (bits == 8) launch_dequant_rows<8, true>(st, cus, dt, q, wd, rows, k);
@@ -339,7 +344,6 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
       check_launch("hb_qlinear (dequantize)");
       QW none{nullptr, nullptr, nullptr, 0, 1};
       mfma_dtype<0, false, false>(dt, geglu, st, cus, pan, X, ldx, wd, none, Bp, Rp, ldr, Yp, ldy, m, n, k);
-      pool_free(ctx, wd);  // stream-ordered: reused only by work enqueued after this GEMM
     } else if (bits == 8 && mode == 0) mfma_dtype<8, false, false>(dt, geglu, st, cu_count(ctx), pan, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
     else if (bits == 8) mfma_dtype<8, true, false>(dt, geglu, st, cu_count(ctx), pan, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
     else if (mode == 0) mfma_dtype<4, false, false>(dt, geglu, st, cu_count(ctx), pan, X, ldx, nullptr, q, Bp, Rp, ldr, Yp, ldy, m, n, k);
