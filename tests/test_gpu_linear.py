@@ -164,13 +164,15 @@ def test_qlinear_config2(b, name, M, bits):
 
 
 @pytest.mark.parametrize("bits", [8, 4])
-@pytest.mark.parametrize("M", [512, 4160])
+@pytest.mark.parametrize("M", [512, 2048, 4160])
 def test_qlinear_bf16(b, M, bits):
     """Quantized weights with bf16 activations: the dequantized weight is
     rounded once to bf16 (quant.ts:189-243, dequantRows then the compute
-    dtype) on both kernels -- M = 512 (the small-M kernel, weight stages
-    loaded two ahead) and M = 4160 (the large-M kernel, a partial row tile) --
-    against the oracle's dequantize-then-linear in bf16, max-rel <= 1e-2."""
+    dtype) on every path -- M = 512 (the 128 x 128 kernel dequantizing in its
+    loader), M = 2048 (the weight dequantized once, then the 128 x 128
+    kernel) and M = 4160 (dequantized once, then the large-M kernel with a
+    partial row tile) -- against the oracle's dequantize-then-linear in bf16,
+    max-rel <= 1e-2."""
     from laya_hip import compose as C
     N, K = SHAPES["Wqkv"]
     rng = np.random.default_rng(7 * M + bits)
