@@ -238,7 +238,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
                                                  const uint8_t* __restrict__ mask, S4 ms, int mask_vec,
                                                  const uint8_t* __restrict__ cls, uint16_t* __restrict__ O, S4 os,
                                                  int Lq, int Lk, float scale_log2, const float2* __restrict__ tabq,
-                                                 const float2* __restrict__ tabk, int pK) {
+                                                 const float2* __restrict__ tabk, int pK, int nqt, int nh) {
   // Q, and two buffers of K and V^T: tile t + 1 is staged while tile t computes
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kBQ * 64];
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * 64];
@@ -247,8 +247,13 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int nqt = gridDim.x, nkt = (Lk + kBK - 1) / kBK;
+  // One block per (b, h, query tile) on a 1-D grid.  The query tiles of one
+  // (b, h) read the same K / V rows and mask bytes: work index order is
+  // query tile fastest, and each XCD takes a contiguous run of work indices,
+  // so those tiles run together on one XCD and share its L2.
+  const int work = xcd_tile(blockIdx.x, gridDim.x);
+  const int qt = work % nqt, bh = work / nqt, h = bh % nh, b = bh / nh;
+  const int nkt = (Lk + kBK - 1) / kBK;
   const int q0 = qt * kBQ;
   const uint16_t* Qb = Q + b * qs.s[0] + h * qs.s[1];
   const uint16_t* Kb = K + b * ks.s[0] + h * ks.s[1];
@@ -656,31 +661,51 @@ extern "C" int hb_sdpa_mask_info(uintptr_t ctx, uintptr_t mask, const int64_t* m
   HB_API_END
 }
 
-// pK > 0: o is the panel-order [B*Lq, pK] matrix (pK = H*D), MFMA path only
-static void sdpa_impl(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
-                      uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info,
-                      uintptr_t o, const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
-                      float scale, double rope_q, double rope_k, int pK) {
+// The MFMA kernel's conditions on a call (else sdpa_simt): 16-bit data,
+// D = 64, unit inner strides, 16-byte aligned rows and 8-element strides, a
+// mask that does not vary over heads, at most kMaxKeyTiles key tiles, and K /
+// V row strides in [0, 2^24) (the kernel adds them as unsigned 24-bit
+// products).  Lk == 0 takes the generic kernel: every row is fully masked,
+// which it gives as 0/0 = NaN, as both kernels do for a row whose keys are
+// all masked, and it needs no mask summary.
+static bool sdpa_takes_mfma(int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks, uintptr_t v,
+                            const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t o, const int64_t* os,
+                            int64_t Lk, int64_t D) {
+  return Lk > 0 && (dt == HB_F16 || dt == HB_BF16) && D == 64 && qs[3] == 1 && ks[3] == 1 && vs[3] == 1 &&
+         os[3] == 1 && q % 16 == 0 && k % 16 == 0 && v % 16 == 0 && o % 8 == 0 && qs[2] % 8 == 0 &&
+         ks[2] % 8 == 0 && vs[2] % 8 == 0 && qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 &&
+         ks[1] % 8 == 0 && vs[0] % 8 == 0 && vs[1] % 8 == 0 && os[0] % 4 == 0 && os[1] % 4 == 0 &&
+         os[2] % 4 == 0 && (mask == 0 || ms[1] == 0) && (Lk + kBK - 1) / kBK <= kMaxKeyTiles && ks[2] >= 0 &&
+         ks[2] < (1 << 24) && vs[2] >= 0 && vs[2] < (1 << 24);
+}
+
+// The argument checks every sdpa entry point makes before it launches
+// anything.
+static void sdpa_check(int dt, const int64_t* qs, const int64_t* ks, const int64_t* vs, uintptr_t mask,
+                       const int64_t* ms, const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) {
   HB_REQUIRE(dt == HB_F32 || dt == HB_F16 || dt == HB_BF16, "hb_sdpa: dtype must be f32, f16 or bf16");
   HB_REQUIRE(qs && ks && vs && os, "hb_sdpa: null strides");
   HB_REQUIRE(!mask || ms, "hb_sdpa: mask without strides");
   HB_REQUIRE(B >= 0 && H >= 0 && Lq >= 0 && Lk >= 0 && D > 0, "hb_sdpa: bad shape");
   HB_REQUIRE(B < 65536 && H < 65536 && Lq < (1 << 30) && Lk < (1 << 30), "hb_sdpa: shape too large");
+}
+
+// pK > 0: o is the panel-order [B*Lq, pK] matrix (pK = H*D), MFMA path only.
+// A masked call on the MFMA path without a summary (mask_info == 0) builds
+// one into a pool block, unless `noalloc`, where that is an error.
+static void sdpa_impl(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uintptr_t k, const int64_t* ks,
+                      uintptr_t v, const int64_t* vs, uintptr_t mask, const int64_t* ms, uintptr_t mask_info,
+                      uintptr_t o, const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
+                      float scale, double rope_q, double rope_k, int pK, bool noalloc = false) {
+  sdpa_check(dt, qs, ks, vs, mask, ms, os, B, H, Lq, Lk, D);
   if (B == 0 || H == 0 || Lq == 0) return;
   HB_REQUIRE((rope_q <= 0 && rope_k <= 0) || D % 2 == 0, "hb_sdpa: rope needs an even head dim");
+  HB_REQUIRE(!noalloc || (rope_q <= 0 && rope_k <= 0), "hb_sdpa_noalloc: no RoPE tables");
   hipStream_t st = stream_of(ctx);
   const float2* tq = rope_q > 0 ? (const float2*)rope_table(ctx, Lq, D, rope_q) : nullptr;
   const float2* tk = rope_k > 0 ? (const float2*)rope_table(ctx, Lk, D, rope_k) : nullptr;
   S4 Qs = s4(qs), Ks = s4(ks), Vs = s4(vs), Ms = s4(ms), Os = s4(os);
-  // No keys (Lk == 0): every row is fully masked; the generic kernel gives
-  // such rows 0/0 = NaN, as it and the MFMA kernel do for a row whose keys
-  // are all masked, and needs no mask summary.
-  bool fast = Lk > 0 && (dt == HB_F16 || dt == HB_BF16) && D == 64 && qs[3] == 1 && ks[3] == 1 && vs[3] == 1 && os[3] == 1 &&
-              q % 16 == 0 && k % 16 == 0 && v % 16 == 0 && o % 8 == 0 && qs[2] % 8 == 0 && ks[2] % 8 == 0 &&
-              vs[2] % 8 == 0 && qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 &&
-              vs[0] % 8 == 0 && vs[1] % 8 == 0 && os[0] % 4 == 0 && os[1] % 4 == 0 && os[2] % 4 == 0 &&
-              (mask == 0 || ms[1] == 0) && (Lk + kBK - 1) / kBK <= kMaxKeyTiles && ks[2] < (1 << 24) &&
-              vs[2] < (1 << 24);
+  const bool fast = sdpa_takes_mfma(dt, q, qs, k, ks, v, vs, mask, ms, o, os, Lk, D);
   if (pK > 0)
     HB_REQUIRE(fast && o % 16 == 0 && pK == H * D,
                "hb_sdpa_panel: needs the MFMA path (f16/bf16, D = 64, aligned operands, mask not varying over heads)");
@@ -691,6 +716,7 @@ static void sdpa_impl(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uin
     int mask_vec = 0;
     if (mask) {
       if (!info) {
+        HB_REQUIRE(!noalloc, "hb_sdpa_noalloc: no mask summary");
         tmp = (uint8_t*)pool_alloc(ctx, mask_info_bytes(B, Lq, Lk));
         launch_mask_info(st, (const uint8_t*)mask, Ms, B, Lq, Lk, tmp);
         check_launch("hb_sdpa(mask info)");
@@ -701,15 +727,17 @@ static void sdpa_impl(uintptr_t ctx, int dt, uintptr_t q, const int64_t* qs, uin
       info = nullptr;
     }
     const float sl2 = scale * 1.4426950408889634f;
-    dim3 grid(nqt, (unsigned)H, (unsigned)B);
+    const int64_t nblk = (int64_t)nqt * H * B;
+    HB_REQUIRE(nblk < ((int64_t)1 << 31), "hb_sdpa: too many (batch, head, query tile) blocks");
+    const unsigned grid = (unsigned)nblk;
     if (dt == HB_F16)
       sdpa_mfma<false><<<grid, kNT, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
                                              (const uint8_t*)mask, Ms, mask_vec, info, (uint16_t*)o, Os, (int)Lq,
-                                             (int)Lk, sl2, tq, tk, pK);
+                                             (int)Lk, sl2, tq, tk, pK, nqt, (int)H);
     else
       sdpa_mfma<true><<<grid, kNT, 0, st>>>((const uint16_t*)q, Qs, (const uint16_t*)k, Ks, (const uint16_t*)v, Vs,
                                             (const uint8_t*)mask, Ms, mask_vec, info, (uint16_t*)o, Os, (int)Lq,
-                                            (int)Lk, sl2, tq, tk, pK);
+                                            (int)Lk, sl2, tq, tk, pK, nqt, (int)H);
     check_launch("hb_sdpa");
     if (tmp) pool_free(ctx, tmp);
   } else {
@@ -748,12 +776,11 @@ extern "C" int hb_sdpa_noalloc(uintptr_t ctx, int dt, uintptr_t q, const int64_t
                                const int64_t* os, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
                                float scale) {
   HB_API_BEGIN
-  HB_REQUIRE(qs && ks && vs && os && (!mask || ms), "hb_sdpa_noalloc: null strides");
-  HB_REQUIRE(B >= 0 && H >= 0 && Lq >= 0 && Lk >= 0 && D > 0 && B < 65536 && H < 65536 && Lq < (1 << 30) &&
-                 Lk < (1 << 30),
-             "hb_sdpa_noalloc: bad shape");
+  sdpa_check(dt, qs, ks, vs, mask, ms, os, B, H, Lq, Lk, D);
   uintptr_t info = 0;
-  if (mask && B > 0 && H > 0 && Lq > 0 && Lk > 0) {
+  // Only a masked call on the MFMA path reads a summary; the others launch
+  // the generic kernel alone and have no size limit here.
+  if (mask && B > 0 && H > 0 && Lq > 0 && sdpa_takes_mfma(dt, q, qs, k, ks, v, vs, mask, ms, o, os, Lk, D)) {
     const size_t need = mask_info_bytes(B, Lq, Lk);
     HB_REQUIRE(need <= kSdpaScratchBytes,
                "hb_sdpa_noalloc: the mask summary needs " + std::to_string(need) + " bytes, more than the " +
@@ -770,7 +797,7 @@ extern "C" int hb_sdpa_noalloc(uintptr_t ctx, int dt, uintptr_t q, const int64_t
     check_launch("hb_sdpa_noalloc(mask info)");
     info = (uintptr_t)p;
   }
-  sdpa_impl(ctx, dt, q, qs, k, ks, v, vs, mask, ms, info, o, os, B, H, Lq, Lk, D, scale, 0.0, 0.0, 0);
+  sdpa_impl(ctx, dt, q, qs, k, ks, v, vs, mask, ms, info, o, os, B, H, Lq, Lk, D, scale, 0.0, 0.0, 0, true);
   HB_API_END
 }
 

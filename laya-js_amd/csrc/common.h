@@ -227,6 +227,17 @@ inline unsigned grid_for(int64_t n, int block) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
+// Blocks are dealt to the 8 XCDs in turn (block b runs on XCD b % 8, each
+// XCD with its own L2).  This maps block `bid` of `nb` to a work index so
+// that every XCD takes one contiguous run of indices, in order: work items
+// next to each other in the index run at the same time on one XCD and share
+// what they read in its L2.
+__device__ __forceinline__ int xcd_tile(int bid, int nb) {
+  int xcd = bid & 7, idx = bid >> 3;
+  int q = nb >> 3, rem = nb & 7;
+  return xcd * q + (xcd < rem ? xcd : rem) + idx;
+}
+
 }  // namespace hb
 
 // Every exported entry point: catch, record the message, return -1.

@@ -50,13 +50,6 @@ __device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
-// Tile index for block `bid` of `nb`: contiguous runs of tiles per XCD.
-__device__ __forceinline__ int xcd_tile(int bid, int nb) {
-  int xcd = bid & 7, idx = bid >> 3;
-  int q = nb >> 3, rem = nb & 7;
-  return xcd * q + (xcd < rem ? xcd : rem) + idx;
-}
-
 // Quantized code e (0..7) of a chunk: q8 codes are bytes of (w0, w1), q4
 // codes nibbles of w0 (even column in the low nibble).
 template <int QB, bool AFF>

@@ -1580,7 +1580,8 @@ class HipBackend:
         panel_ok = (dt in ("f16", "bf16") and D == 64 and Lk > 0 and (H * D) % 64 == 0
                     and all(p % 16 == 0 for p in (qp, kp, vp)) and all(st_[3] == 1 for st_ in (qs, ks, vs))
                     and all(st_[i] % 8 == 0 for st_ in (qs, ks, vs) for i in range(3))
-                    and (ms is None or ms[1] == 0) and (Lk + 63) // 64 <= 1024)
+                    and (ms is None or ms[1] == 0) and (Lk + 63) // 64 <= 1024
+                    and 0 <= ks[2] < 1 << 24 and 0 <= vs[2] < 1 << 24)
         args = (DT[dt][0], qp, qs, kp, ks, vp, vs, mp, ms, info, B, H, Lq, Lk, D, float(scale), rq, rk)
         pend = _PendingSdpa(self, args, refs, panel_ok)
         if mc is not None and mc is not mask:
@@ -1609,11 +1610,17 @@ class HipBackend:
             self._call("sdpa", "hb_alloc", self.ctx, max(1, n.value), F.C.byref(p))
             ent = cache[key] = [p.value, False]
         rec = self._capture_summaries
-        if not ent[1] or (rec is not None and (id(mc._st), key) not in rec):
+        if rec is not None:
+            # Recorded, not run: only a replay writes this summary, so the
+            # entry's freshness is left as it was (an entry first built
+            # inside a recording stays stale and an eager call after the
+            # recording, or after an aborted one, rebuilds it).
+            if (id(mc._st), key) not in rec:
+                self._call("sdpa", "hb_sdpa_mask_info", self.ctx, self._ptr(mc), F.i64s(ms), B, Lq, Lk, ent[0])
+                rec.add((id(mc._st), key))
+        elif not ent[1]:
             self._call("sdpa", "hb_sdpa_mask_info", self.ctx, self._ptr(mc), F.i64s(ms), B, Lq, Lk, ent[0])
             ent[1] = True
-            if rec is not None:
-                rec.add((id(mc._st), key))
         return ent[0]
 
     def write(self, t: HipTensor, h: HostTensor) -> None:

@@ -258,6 +258,25 @@ def _shape_str(s) -> str:
     return ",".join(str(int(d)) for d in s)
 
 
+def validateConfig(cfg, enc: ModernBertConfig) -> None:
+    """`Agent.__init__`'s config check (agent.ts:96-105), run by load()
+    before any weight is read (load.ts:53): the config names its encoder and
+    head layers, and 4 < head_max_len < max_len <= the encoder's position
+    limit (defaults 192 and 512).  Raises with the reference's messages."""
+    if not isinstance(cfg, dict) or "encoder" not in cfg or "head_layers" not in cfg:
+        raise ValueError("Laya config must specify encoder and head_layers")
+    max_len = cfg.get("max_len")
+    head_max_len = cfg.get("head_max_len")
+    max_len = 512 if max_len is None else max_len
+    head_max_len = 192 if head_max_len is None else head_max_len
+    try:
+        ok = 4 < head_max_len < max_len <= enc.maxPositionEmbeddings
+    except TypeError:
+        ok = False
+    if not ok:
+        raise ValueError("Expected 4 < head_max_len < max_len <= max_position_embeddings")
+
+
 def loadDecisionModel(backend, encoderConfig, agentConfig: dict, weights, dtype: str = "f32") -> DecisionModel:
     """model.ts:283-338: loads the encoder (names under "encoder.") and the
     decision-head weights; every name and shape is checked before the
@@ -338,6 +357,7 @@ def loadCheckpoint(backend, path: str, dtype: str = "f32", quantized: str = "dev
         agent_cfg = json.load(fh)
     with open(os.path.join(path, "encoder", "config.json")) as fh:
         enc_cfg = json.load(fh)
+    validateConfig(agent_cfg, parseModernBertConfig(enc_cfg))  # before reading weights (load.ts:53)
     weights = read_weights(os.path.join(path, "model.safetensors"), dtype=dtype, quantized=quantized)
     model = loadDecisionModel(backend, enc_cfg, agent_cfg, weights.get, dtype=dtype)
     extra = [n for n in weights.remaining() if n != "temperature"]

@@ -164,3 +164,37 @@ def test_device_getter_hands_out_packed_matrices(bits):
         np.testing.assert_array_equal(np.asarray(ref.data).view(np.uint16).reshape(h.shape), want)
     plain = dev.get("encoder.final_norm.weight")
     assert isinstance(plain, HostTensor) and plain.dtype == "f32"
+
+
+@pytest.mark.parametrize("patch,msg", [
+    ({"head_layers": None}, "must specify encoder and head_layers"),
+    ({"encoder": None}, "must specify encoder and head_layers"),
+    ({"head_max_len": 4}, "4 < head_max_len < max_len"),
+    ({"head_max_len": 128}, "4 < head_max_len < max_len"),
+    ({"max_len": 257}, "4 < head_max_len < max_len"),
+])
+def test_load_checkpoint_validates_the_config_before_reading_weights(tmp_path, patch, msg):
+    """load.ts:53 runs validateConfig (agent.ts:96-105) before any weight is
+    read: an invalid rl_agent_config.json fails with the reference's message
+    even when model.safetensors is unreadable, and no backend call is made
+    (the backend argument is None)."""
+    import json
+    import shutil
+    from laya_hip.model import loadCheckpoint, validateConfig
+    from laya_hip.modernbert import parseModernBertConfig
+
+    src = os.path.dirname(TINY)
+    d = tmp_path / "ckpt"
+    shutil.copytree(src, d)
+    cfg = json.load(open(d / "rl_agent_config.json"))
+    enc = parseModernBertConfig(json.load(open(d / "encoder" / "config.json")))
+    validateConfig(cfg, enc)  # the fixture's own config is valid
+    for k, v in patch.items():
+        if v is None:
+            del cfg[k]
+        else:
+            cfg[k] = v
+    json.dump(cfg, open(d / "rl_agent_config.json", "w"))
+    (d / "model.safetensors").write_bytes(b"not a safetensors file")
+    with pytest.raises(ValueError, match=msg):
+        loadCheckpoint(None, str(d))

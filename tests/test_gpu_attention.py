@@ -149,3 +149,40 @@ def test_sdpa_generic_path_matches_oracle(b):
         got = read32(b, b.sdpa(b.rope(dev[0], 10000.0), dev[1], dev[2], b.fromHost(sliding), 0.25))
         ref = cr.sdpa(cr.rope(q, 10000.0), k, v, sliding.data, 0.25)
         np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_sdpa_negative_key_and_value_row_strides(b):
+    """hb_sdpa through the C ABI with K and V given as row-reversed views (the
+    base pointer at their last row, row stride -64 elements), otherwise
+    meeting every condition of the MFMA kernel: the call takes the generic
+    kernel, which addresses negative strides, and matches the oracle on the
+    reversed keys and values.  Also a masked call."""
+    from laya_hip import ffi as F
+    rng = np.random.default_rng(12)
+    B, H, L, D = 2, 3, 192, 64
+    valid = np.ones((B, L), np.uint8)
+    valid[1, 130:] = 0
+    full, sliding = attentionMasks(valid, B, L, 128)
+    x = [rounded(rng.standard_normal((B, H, L, D)), "f16") for _ in range(3)]
+    q, k, v = (b.fromHost(to_host(a, "f16")) for a in x)
+    out = b._malloc(B * H * L * D * 2)
+    for mh in (None, sliding):
+        m = None if mh is None else b.fromHost(mh)
+        print(f"sdpa negative strides mask={mh is not None}", flush=True)
+        st = F.i64s((H * L * D, L * D, D, 1))
+        rev = F.i64s((H * L * D, L * D, -D, 1))
+        last = (L - 1) * D * 2  # bytes to the last row of a (b, h) block
+        mp, ms = (0, None) if m is None else (b._ptr(m), F.i64s((L * L, 0, L, 1)))
+        b.n.call("sdpa", "hb_sdpa", b.ctx, F.HB_F16, b._ptr(q), st, b._ptr(k) + last, rev, b._ptr(v) + last, rev,
+                 mp, ms, 0, out.ptr, st, B, H, L, L, D, 0.125, 0.0, 0.0)
+        got = np.empty(B * H * L * D, np.uint16)
+        b.n.call("read", "hb_download", b.ctx, got.ctypes.data, out.ptr, got.nbytes)
+        got = got.view(np.float16).astype(np.float32).reshape(B, H, L, D)
+        ref = cr.sdpa(x[0], x[1][:, :, ::-1].copy(), x[2][:, :, ::-1].copy(),
+                      None if mh is None else mh.data, 0.125)
+        assert max_rel(got, ref) <= 5e-3
+        if m is not None:
+            b.dispose(m)
+    for t in (q, k, v):
+        b.dispose(t)
+    out.release()

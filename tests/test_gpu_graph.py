@@ -172,3 +172,51 @@ def test_recording_refuses_synchronizing_calls(b):
     np.testing.assert_array_equal(np.asarray(b.read(y).data).reshape(4, 64), np.full((4, 64), 3.0, np.float32))
     for t in (x, y):
         b.dispose(t)
+
+
+def test_summary_recorded_without_warmup_is_rebuilt_eagerly(b):
+    """Mask summaries first enqueued inside a recording (capture with
+    warmup=False, and a recording that raises part-way) are written only by a
+    replay: an eager forward on the same masks afterwards rebuilds them and
+    gives the bits of a forward on a fresh upload of the same inputs."""
+    B, T = 2, 256
+    rng = np.random.default_rng(77)
+    W = _weights(rng)
+    enc = loadModernBert(b, parseModernBertConfig(CFG),
+                         lambda nm: HostTensor("f16", W[nm[8:]].shape, W[nm[8:]])
+                         if nm.startswith("encoder.") and nm[8:] in W else None, dtype="f16")
+    ids = rng.integers(0, CFG["vocab_size"], (B, T)).astype(np.int32)
+    valid = np.ones((B, T), np.uint8)
+    valid[0, 150:] = 0
+    valid[1, 40:] = 0
+
+    def run(inp):
+        y = enc.encode(inp)
+        out = _bits(b, y)
+        b.dispose(y)
+        return out
+
+    ref_inp = enc.uploadInputs(ids, valid, B, T)
+    want = run(ref_inp)  # also sets up the RoPE tables outside any recording
+    enc.disposeInputs(ref_inp)
+
+    inp = enc.uploadInputs(ids, valid, B, T)
+    g = b.capture(lambda: enc.encode(inp), warmup=False)
+    np.testing.assert_array_equal(run(inp), want)  # eager, before any replay
+    np.testing.assert_array_equal(_bits(b, g.run()), want)
+    out = g.out
+    g.destroy()
+    b.dispose(out)
+    enc.disposeInputs(inp)
+
+    inp2 = enc.uploadInputs(ids, valid, B, T)
+
+    def aborts():
+        enc.encode(inp2)
+        raise KeyError("abort the recording")
+
+    with pytest.raises(KeyError):
+        b.capture(aborts, warmup=False)
+    np.testing.assert_array_equal(run(inp2), want)
+    enc.disposeInputs(inp2)
+    enc.dispose()
