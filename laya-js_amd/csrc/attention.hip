@@ -247,12 +247,24 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4))) void s
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  // One block per (b, h, query tile) on a 1-D grid.  The query tiles of one
-  // (b, h) read the same K / V rows and mask bytes: work index order is
-  // query tile fastest, and each XCD takes a contiguous run of work indices,
-  // so those tiles run together on one XCD and share its L2.
-  const int work = xcd_tile(blockIdx.x, gridDim.x);
-  const int qt = work % nqt, bh = work / nqt, h = bh % nh, b = bh / nh;
+  // One block per (b, h, query tile) on a 1-D grid.  Blocks are dealt to the
+  // 8 XCDs in turn (block i on XCD i % 8).  The query tiles of one (b, h)
+  // read the same K / V rows and mask bytes, so they go to one XCD as
+  // consecutive blocks of its share (they run together and share its L2),
+  // and the (b, h) pairs are dealt to the XCDs in turn, which spreads
+  // sequences of different lengths (and work) evenly over them.  Without a
+  // multiple of 8 pairs the blocks take (b, h, query tile) in order.
+  const int nbh = (int)(gridDim.x / nqt);
+  int qt, bh;
+  if ((nbh & 7) == 0) {
+    const int x = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    qt = idx % nqt;
+    bh = (idx / nqt) * 8 + x;
+  } else {
+    qt = blockIdx.x % nqt;
+    bh = blockIdx.x / nqt;
+  }
+  const int h = bh % nh, b = bh / nh;
   const int nkt = (Lk + kBK - 1) / kBK;
   const int q0 = qt * kBQ;
   const uint16_t* Qb = Q + b * qs.s[0] + h * qs.s[1];

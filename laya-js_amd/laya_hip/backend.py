@@ -468,17 +468,27 @@ class _PendingSdpa:
 
 # ------------------------------------------------------------------ recorded graphs
 
+def _flat_outputs(out, op: str) -> list:
+    """The tensors of a tensor, list or tuple result."""
+    ts = [out] if isinstance(out, HipTensor) else list(out) if isinstance(out, (list, tuple)) else None
+    if ts is None or not all(isinstance(t, HipTensor) for t in ts):
+        raise TypeError(f"{op}: the function must return a tensor or a list / tuple of tensors")
+    return ts
+
+
 class HipGraph:
     """An op sequence recorded by HipBackend.capture.  run() replays it on
-    the backend's stream and returns the output tensor (the same one each
-    time, rewritten by the replay; it belongs to the caller, who disposes it
+    the backend's stream and returns the output (a tensor, or the list /
+    tuple the recorded function returned: the same tensors each time,
+    rewritten by the replay; they belong to the caller, who disposes them
     after destroy())."""
 
-    def __init__(self, be: "HipBackend", exec_: int, out: HipTensor, held: list):
+    def __init__(self, be: "HipBackend", exec_: int, out, held: list):
         self.be, self.exec, self.out, self.held = be, exec_, out, held
-        self._st = out._st.retain() if out._st is not None else None  # the graph writes it
+        # the graph writes them
+        self._sts = [t._st.retain() for t in _flat_outputs(out, "capture") if t._st is not None]
 
-    def run(self) -> HipTensor:
+    def run(self):
         if not self.exec or self.be._destroyed:
             raise RuntimeError("HipGraph: used after destroy()")
         self.be._call("graph", "hb_graph_launch", self.be.ctx, self.exec)
@@ -494,9 +504,9 @@ class HipGraph:
                 be._recycle(ptr, nbytes)
         self.held = []
         self.exec = 0
-        if self._st is not None:
-            self._st.release()
-            self._st = None
+        for st in self._sts:
+            st.release()
+        self._sts = []
 
 
 # ------------------------------------------------------------------ backend
@@ -525,6 +535,7 @@ class HipBackend:
         self._blocks: dict[int, list[int]] = {}
         self._capture_held: Optional[list] = None  # blocks disposed while a capture records
         self._capture_summaries: Optional[set] = None  # summaries already enqueued into the recording
+        self._compiled: list = []  # release functions of compile() wrappers
         self._cus: Optional[int] = None  # compute units, read once (HipBackend.cus)
         self.stats = {"linear": 0, "linear_fused_geglu": 0, "linear_fused_resid": 0, "linear_fused_qkv": 0, "sdpa": 0,
                       "sdpa_fused_rope": 0, "copies": 0, "panel_unpacks": 0}
@@ -923,6 +934,9 @@ class HipBackend:
 
     def destroy(self) -> None:
         if not self._destroyed:
+            for release in self._compiled:
+                release()
+            self._compiled = []
             self._blocks.clear()  # the library frees every block with the context
             self._call("destroy", "hb_destroy", self.ctx)
             self._destroyed = True
@@ -939,11 +953,15 @@ class HipBackend:
         the inputs (mask tile classes) are recomputed by every replay.
         `warmup` runs `fn` once eagerly first, so one-time set-up that
         allocates or uploads (RoPE tables, summary buffers) happens outside
-        the recording."""
+        the recording.  `fn` returns a tensor or a list / tuple of tensors."""
         if self._capture_held is not None:
             raise RuntimeError("capture: already recording")
         if warmup:
-            self.dispose(self._ready(fn()))
+            done = set()
+            for t in _flat_outputs(fn(), "capture"):
+                if id(t) not in done:
+                    done.add(id(t))
+                    self.dispose(self._ready(t))
         self.flush()
         held: list = []
         self._capture_held = held
@@ -952,7 +970,8 @@ class HipBackend:
         e = F.U(0)
         try:
             out = fn()
-            self._ready(out)  # the result's pending launches belong to the recording
+            for t in _flat_outputs(out, "capture"):
+                self._ready(t)  # the result's pending launches belong to the recording
         except BaseException:
             self._capture_held = None
             self._capture_summaries = None
@@ -973,6 +992,64 @@ class HipBackend:
                 self._recycle(ptr, nbytes)
             raise
         return HipGraph(self, e.value, out, held)
+
+    def compile(self, fn: Callable) -> Callable:
+        """Backend.compile (tensor-backend/src/index.ts:245): wraps `fn`, a
+        pure function of tensors returning a tensor or a list / tuple of
+        tensors, for replay.  The first call with a given input signature
+        (shapes and dtypes) copies its inputs into blocks of their own and
+        records `fn` on those (HipBackend.capture); every call copies its
+        inputs into its signature's blocks, replays that recording and
+        returns fresh copies of the outputs in `fn`'s structure, which the
+        caller owns.  A replay re-derives the device summaries of its inputs
+        (attention-mask tile classes).  The recordings and their blocks live
+        until the wrapper's `release()` or the backend's destroy()."""
+        recs: dict = {}
+
+        def run(*args):
+            if self._capture_held is not None:
+                raise RuntimeError("compile: called while a graph records")
+            self._live(*args, op="compile")
+            key = tuple((tuple(t.shape), t.dtype) for t in args)
+            rec = recs.get(key)
+            if rec is None:
+                # input blocks of the recording: untracked, owned by the wrapper
+                ins = [HipTensor(tuple(t.shape), t.dtype, self._malloc(max(1, _numel(t.shape)) * DT[t.dtype][1]))
+                       for t in args]
+                for src, dst in zip(args, ins):
+                    if src.size:
+                        self._copy_into(src, dst._st.ptr, None)
+                g = self.capture(lambda: fn(*ins))
+                rec = recs[key] = (ins, g)
+            else:
+                ins, g = rec
+                for src, dst in zip(args, ins):
+                    if src.size:
+                        self._copy_into(src, dst._st.ptr, None)
+                    for ent in (dst._st.cache or {}).values():
+                        ent[1] = False  # summaries of the old contents
+            out = g.run()
+            copies = []
+            for t in _flat_outputs(out, "compile"):
+                c = self._new(t.shape, t.dtype)
+                if t.size:
+                    self._copy_into(t, c._st.ptr, None)
+                copies.append(c)
+            if isinstance(out, HipTensor):
+                return copies[0]
+            return type(out)(copies)
+
+        def release() -> None:
+            for ins, g in recs.values():
+                outs = _flat_outputs(g.out, "compile")
+                g.destroy()
+                for t in ins + outs:
+                    self.dispose(t)
+            recs.clear()
+
+        run.release = release
+        self._compiled.append(release)
+        return run
 
     def pool_stats(self) -> dict:
         self._return_blocks()  # blocks waiting for reuse count as cached, not live

@@ -168,6 +168,28 @@ class DecisionModel:
         out = b.scope(f)
         return out[0], out[1]
 
+    _INPUTS = ("inputIds", "fullMask", "slidingMask", "headMask", "qtype", "markerPos", "markerMask", "k")
+
+    def compiled(self) -> Optional[Callable]:
+        """model.ts:250-275: a forwardTensors equivalent through
+        `backend.compile` (recorded once per input shape signature); None
+        when the backend has no compile.  No stage observation."""
+        b = self.backend
+        if getattr(b, "compile", None) is None:
+            return None
+        names = self._INPUTS
+        fn = b.compile(lambda *ts: list(self.forwardCore(dict(zip(names, ts)))))
+
+        def run(batch: Batch):
+            inp = self.uploadBatch(batch)
+            try:
+                logits, act = fn(*(inp[n] for n in names))
+                return logits, act
+            finally:
+                self.disposeInputs(inp)
+        run.release = fn.release  # frees the recordings (HipBackend.compile)
+        return run
+
     def forwardTensors(self, batch: Batch, onStage: Optional[Callable] = None):
         """model.ts:242-249: (logits, act) device tensors; caller disposes."""
         inp = self.uploadBatch(batch)

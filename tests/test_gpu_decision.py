@@ -249,3 +249,78 @@ def test_base_decision_model_logits_and_argmax_match_oracle(b):
     assert np.array_equal(np.argmax(np.where(mm != 0, logits, -np.inf), 1),
                           np.argmax(np.where(mm != 0, ref_lg, -np.inf), 1))
     model.dispose()
+
+
+def _eager_and_compiled(model, batches):
+    """Eager forward and the `compiled()` forward (model.ts:250-275) on each
+    batch: (eager logits, eager act, compiled logits, compiled act) bits."""
+    b = model.backend
+    run = model.compiled()
+    assert run is not None, "HipBackend has compile, so compiled() returns a function"
+    out = []
+    for batch in batches:
+        e = model.forward(batch)
+        lg, ac = run(batch)
+        c = model.readOutputs((lg, ac))
+        out.append((e["logits"], e["act"], c["logits"], c["act"]))
+    run.release()
+    return out
+
+
+def test_compiled_tiny_decision_model_equals_eager_bits(b):
+    """DecisionModel.compiled() on HipBackend (Backend.compile over
+    HipBackend.capture): the first call records, later calls of the same
+    shape copy their inputs into the recorded blocks and replay.  Every
+    call gives the eager forward's bits, also after the batch's ids,
+    markers and padding change; after release() and destroy of the model
+    the pool holds no block of the model's calls."""
+    act = _json("activations.json")
+    model = loadDecisionModel(b, _json("encoder", "config.json"), _json("rl_agent_config.json"),
+                              read_weights(os.path.join(TINY, "model.safetensors")).get)
+    blocks = b.pool_stats()["live_blocks"]
+    base = _tiny_batch(act, M=3)
+    rng = np.random.default_rng(3)
+    B, L = base.size, base.length
+    other = Batch(B, L, 3, rng.integers(0, 128, (B, L)).astype(np.int32), base.attentionMask.copy(),
+                  base.markerPos.copy(), base.markerMask.copy(), base.qtype.copy())
+    other.attentionMask[0, L // 2:] = 0
+    other.markerPos[0] = np.minimum(other.markerPos[0], L // 2 - 1)
+    runs = _eager_and_compiled(model, [base, other, base])
+    for i, (el, ea, cl, ca) in enumerate(runs):
+        np.testing.assert_array_equal(cl.view(np.uint32), el.view(np.uint32), err_msg=f"logits, call {i}")
+        np.testing.assert_array_equal(ca.view(np.uint32), ea.view(np.uint32), err_msg=f"act, call {i}")
+    assert not np.array_equal(runs[0][0], runs[1][0])
+    model.dispose()
+    assert b.pool_stats()["live_blocks"] <= blocks
+
+
+def test_compiled_base_decision_model_equals_eager_with_a_new_mask(b):
+    """The compiled forward at the ModernBERT-base shape (22 layers, f16,
+    B = 4, L = 128): the same bits as the eager forward on two batches of
+    one shape whose padding (and so every attention mask and the mask
+    summaries recorded into the graph) differs between the calls."""
+    rng = np.random.default_rng(8)
+    W = _base_decision_weights(rng)
+    enc_cfg = {"vocab_size": 50368, "hidden_size": 768, "intermediate_size": 1152, "num_hidden_layers": 22,
+               "num_attention_heads": 12, "local_attention": 128}
+    agent = {"head_layers": 2, "act_costs": {"escalate": 0.5, "defer": 0.25}}
+    model = loadDecisionModel(b, enc_cfg, agent, lambda n: HostTensor("f16", W[n].shape, W[n].astype(np.float16))
+                              if n in W else None, dtype="f16")
+    B, L, M = 4, 128, 8
+    batches = []
+    for lens in ([128, 97, 64, 120], [40, 128, 111, 77]):
+        lens = np.array(lens)
+        ids = rng.integers(0, 50368, (B, L)).astype(np.int32)
+        valid = (np.arange(L)[None, :] < lens[:, None]).astype(np.uint8)
+        pos = np.zeros((B, M), np.int32)
+        mm = np.zeros((B, M), np.uint8)
+        for r in range(B):
+            nm = int(rng.integers(2, M + 1))
+            pos[r, :nm] = np.sort(rng.choice(np.arange(1, lens[r]), nm, replace=False))
+            mm[r, :nm] = 1
+        batches.append(Batch(B, L, M, ids, valid, pos, mm, rng.integers(0, 3, B).astype(np.int32)))
+    for i, (el, ea, cl, ca) in enumerate(_eager_and_compiled(model, batches)):
+        print(f"compiled base decision model, call {i}: logits {cl.reshape(B, M)[:, :2].tolist()}")
+        np.testing.assert_array_equal(cl.view(np.uint32), el.view(np.uint32), err_msg=f"logits, call {i}")
+        np.testing.assert_array_equal(ca.view(np.uint32), ea.view(np.uint32), err_msg=f"act, call {i}")
+    model.dispose()
