@@ -1471,6 +1471,21 @@ void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int
       }
     }
     HB_REQUIRE(pan == 0, "hb_linear: panel-order operands on a kernel that does not take them");
+    // Tiles of 128 x 64 (waves of 32 x 64) where 128 x 128 tiles would
+    // leave the GPU short of blocks: the K stages of a block run one after
+    // another (each one's loads, LDS staging and barrier), so a launch with
+    // few blocks is bound by that chain; halving the tile halves the work
+    // of each stage.  Measured (16-bit, M = 2048): attn Wo 18.2 -> 14.3 us,
+    // mlp Wo 22.9 -> 18.1 us; at M = 3072 the 2304-column shapes are faster
+    // with 128 x 128 tiles (27.0 against 32.8 us).  Every output keeps its
+    // MFMA sequence and epilogue, so the bits do not change.
+    if constexpr (QB == 0) {
+      const int64_t t128 = ((M + 127) / 128) * ((N + (GEGLU ? 63 : 127)) / (GEGLU ? 64 : 128));
+      if (t128 <= cus + cus / 8) {
+        launch_mfma<128, 64, 4, 1, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+        return;
+      }
+    }
     launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   }
 }
