@@ -1221,8 +1221,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     load_b(tile_n0(i1), k1, B1);
     __syncthreads();
   }
-  // The register rotation has period 6, so a block streams several tiles
-  // only when KT % 6 == 0 (the launcher gives every block one tile otherwise).
+  // The register rotation has period 6; a tile whose KT is not a multiple of
+  // 6 ends with a tail that moves the next tile's registers back to phase 0.
   for (int it = 0; it < ntile; it++) {
     const int g0 = it * KT;
     cur_m0 = tile_m0(it);
@@ -1268,17 +1268,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       step(I4{}, F{}, g0 + kt + 4, kt + 4, A1, A0, B0, B1);
       step(I5{}, F{}, g0 + kt + 5, kt + 5, A2, A1, B1, B0);
     }
-    // The last KT % 6 stages: blocks with one tile only (the launcher
-    // streams several tiles per block only when KT % 6 == 0).  Every load
-    // is drained after them, so the join after this tail leaves the
-    // compiler's view of the loads in flight exactly that of the loop above.
+    // The last q = KT % 6 stages.  Every load is drained after them, so the
+    // join after this tail leaves the compiler's view of the loads in flight
+    // exactly that of the loop above.  The next tile's first two stages are
+    // then in registers named by phase q (its stage-0 X rows in set q % 3,
+    // its stage-1 X rows in set (q + 1) % 3, its stage-1 W in set
+    // (q + 1) % 2): they are moved to the names the tile loop starts from
+    // (A0, A1, B1), so that every tile starts at phase 0 whatever KT is.
     if (kt < KT) {
+      const int q = KT - kt;
       step(I0{}, F{}, g0 + kt, kt, A0, A2, B0, B1);
-      if (kt + 1 < KT) step(I1{}, F{}, g0 + kt + 1, kt + 1, A1, A0, B1, B0);
-      if (kt + 2 < KT) step(I2{}, F{}, g0 + kt + 2, kt + 2, A2, A1, B0, B1);
-      if (kt + 3 < KT) step(I3{}, F{}, g0 + kt + 3, kt + 3, A0, A2, B1, B0);
-      if (kt + 4 < KT) step(I4{}, F{}, g0 + kt + 4, kt + 4, A1, A0, B0, B1);
+      if (q > 1) step(I1{}, F{}, g0 + kt + 1, kt + 1, A1, A0, B1, B0);
+      if (q > 2) step(I2{}, F{}, g0 + kt + 2, kt + 2, A2, A1, B0, B1);
+      if (q > 3) step(I3{}, F{}, g0 + kt + 3, kt + 3, A0, A2, B1, B0);
+      if (q > 4) step(I4{}, F{}, g0 + kt + 4, kt + 4, A1, A0, B0, B1);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      if (has_next) {
+        if (q % 3 == 1) {  // stage 0 in A1, stage 1 in A2 (A0 is free)
+#pragma unroll
+          for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int s = 0; s < KS; s++) {
+              A0[i][s] = A1[i][s];
+              A1[i][s] = A2[i][s];
+            }
+        } else if (q % 3 == 2) {  // stage 0 in A2, stage 1 in A0 (A1 is free)
+#pragma unroll
+          for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int s = 0; s < KS; s++) {
+              A1[i][s] = A0[i][s];
+              A0[i][s] = A2[i][s];
+            }
+        }
+        if (q & 1) B1 = B0;  // stage-1 W in B0
+      }
     }
     // The residual's last pieces went out at the end of stage dma0 + dpl, and
     // memory operations complete in issue order: they have landed once at
@@ -1349,11 +1373,14 @@ void launch_arow(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64
                  QK qk = QK{nullptr, 1, 1}) {
   constexpr int BNO = GEGLU ? BN / 2 : BN;
   const int tiles_m = (M + 255) / 256, tiles_n = (N + BNO - 1) / BNO, tiles = tiles_m * tiles_n;
-  // one persistent block per CU, a multiple of 8 (one per XCD); with
-  // K % 384 != 0 at most one tile per block: every XCD gets as many blocks
-  // as the largest XCD share of tiles (ceil(tiles_m / 8) row panels)
+  // one persistent block per CU, a multiple of 8 (one per XCD), streaming
+  // its tiles when they have a multiple of 6 or at least 12 K stages (the
+  // shapes measured and tested).  Otherwise one tile per block: every XCD
+  // gets as many blocks as the largest XCD share of tiles (ceil(tiles_m / 8)
+  // row panels).
   const int KT = (K + 63) / 64;
-  int grid = KT % 6 == 0 ? (tiles < cus ? tiles : cus) / 8 * 8 : 8 * (((tiles_m + 7) / 8) * tiles_n);
+  const bool stream = KT % 6 == 0 || KT >= 12;
+  int grid = stream ? (tiles < cus ? tiles : cus) / 8 * 8 : 8 * (((tiles_m + 7) / 8) * tiles_n);
   HB_REQUIRE(grid >= 8, "hb_linear: large-M GEMM needs at least 8 tiles");
   constexpr int RG = (BNO / 8 + 7) / 8;
   // W tiles and the C tile

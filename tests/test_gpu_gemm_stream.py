@@ -1,10 +1,12 @@
 """The large-M GEMM with several tiles per block, on the GPU, through the C ABI.
 
-When a block streams several output tiles (K a multiple of 384 and more
-tiles than CUs), an interior tile's output leaves during the next tile's
-first stages instead of in one burst, and a residual tile is copied in from
-a later stage; edge tiles (ragged M or N) and outputs in the other layout
-still leave in one burst.  Each case checks:
+When a block streams several output tiles (more tiles than CUs, and K stages
+that are a multiple of 6 or at least 12), an interior tile's output leaves
+during the next tile's first stages instead of in one burst, and a residual
+tile is copied in from a later stage; edge tiles (ragged M or N) and outputs
+in the other layout still leave in one burst.  A tile whose K stages are not
+a multiple of 6 ends with a tail that hands the next tile's registers over
+(every remainder 1..5 is covered).  Each case checks:
 - bit for bit, 128-row windows of the output (first, middle, last rows)
   against hb_linear on those 128 rows alone, which takes the small-M
   kernels: every MFMA kernel gives a row the same bits;
@@ -60,6 +62,12 @@ CASES = [
     (32768, 768, 768, False, True, True),     # two tiles per block with bias and residual
     (32768, 768, 1152, False, False, True),   # mlp Wo shape, K = 1152, residual
     (16384, 2304, 768, True, False, False),   # GeGLU, row-major output
+    (16384, 2304, 1024, False, False, False),  # 16 K stages (a tail of 4), the large config's Wqkv
+    (32768, 1024, 1024, False, True, True),    # the large config's attn Wo: partial last column tile
+    (32768, 1024, 2624, False, False, True),   # the large config's mlp Wo: 41 stages (a tail of 5)
+    (16384, 2304, 832, True, False, False),    # GeGLU, 13 stages (a tail of 1)
+    (16384, 2304, 896, False, True, False),    # 14 stages (a tail of 2)
+    (8192, 2304, 960, False, False, True),     # 15 stages (a tail of 3), residual
 ]
 
 
@@ -99,16 +107,17 @@ def test_streamed_tiles_equal_single_tile_rows(b, dtype, M, N, K, geglu, bias, r
             b.dispose(t)
 
 
+@pytest.mark.parametrize("K", [768, 1024])
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_streamed_panel_output_equals_row_major(b, dtype, bias):
+def test_streamed_panel_output_equals_row_major(b, dtype, bias, K):
     """The GeGLU linear with its output in panel order (streamed, as the
     encoder's Wi runs: an interior tile's GELU products are formed while the
     next tile computes) equals the row-major output (every GELU in the
     epilogue) bit for bit, with x row-major and in panel order, with and
-    without a bias."""
-    print(f"streamed GeGLU panel output {dtype} bias={bias}", flush=True)
-    M, N, K = 16384, 2304, 768
+    without a bias, at 12 K stages and at 16 (a tail of 4 per tile)."""
+    print(f"streamed GeGLU panel output {dtype} bias={bias} K={K}", flush=True)
+    M, N = 16384, 2304
     rng = np.random.default_rng(5)
     dt = F.HB_F16 if dtype == "f16" else F.HB_BF16
     x = rounded(rng.standard_normal((M, K)), dtype)
