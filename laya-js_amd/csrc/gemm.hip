@@ -323,12 +323,15 @@ extern "C" int hb_qlinear(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintp
     int m = (int)M, n = (int)N, k = (int)K;
     const int cus0 = cu_count(ctx);
     const bool slab = slab_path(M, N, K, geglu, cus0) && qslab_ok(K, geglu ? 2 : 1, bits, mode == 1, q);
-    if (arow_path(M) || (M >= 1024 && !slab)) {
-      // From M = 1024 (unless the slab kernel takes the call): the weight is
-      // dequantized once into a pooled 16-bit copy and the 16-bit GEMM runs
-      // on it.  A loader that dequantizes repeats the work for every row
-      // tile (at M = 8192: 22-34% over 16-bit weights, against one
-      // bandwidth-bound pass over the weight here).
+    if (arow_path(M) || (M >= 1024 && !slab && !thin_tiles(M, N, geglu, cus0))) {
+      // At M >= 4096, and from M = 1024 where neither the slab kernel nor
+      // 128 x 64 tiles take the call: the weight is dequantized once into a
+      // pooled 16-bit copy and the 16-bit GEMM runs on it.  A loader that
+      // dequantizes repeats the work for every row tile (at M = 8192:
+      // 22-34% over 16-bit weights, against one bandwidth-bound pass over
+      // the weight here).  With 128 x 64 tiles (many blocks, each a short
+      // chain of K stages) the loader's dequantization is the faster of the
+      // two (M = 2048: Wo 16.3 -> 14.6, Wqkv 27.9 -> 24.6 us).
       const int64_t rows = geglu ? 2 * N : N;
       struct PoolBlock {  // back to the pool when the call ends, by return or throw
         uintptr_t ctx;

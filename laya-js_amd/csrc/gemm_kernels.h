@@ -1470,6 +1470,14 @@ inline bool slab_path(int64_t M, int64_t N_out, int64_t K, bool geglu, int cus) 
 // the call takes one of them before dispatching.
 inline bool arow_path(int64_t M) { return M >= 4096; }
 
+// Below M = 4096, without the slab kernel: 128 x 64 tiles (instead of
+// 128 x 128) where 128 x 128 tiles would leave the GPU short of blocks.
+// N_out: output columns (GeGLU: value / gate pairs).
+inline bool thin_tiles(int64_t M, int64_t N_out, bool geglu, int cus) {
+  const int64_t t128 = ((M + 127) / 128) * ((N_out + (geglu ? 63 : 127)) / (geglu ? 64 : 128));
+  return t128 <= cus + cus / 8;
+}
+
 template <bool BF16, bool GEGLU, int QB, bool AFF, bool SF32>
 void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int64_t ldx, const uint16_t* w,
                           QW qw, const uint16_t* bias, const uint16_t* r, int64_t ldr, uint16_t* y, int64_t ldy, int M,
@@ -1505,13 +1513,13 @@ void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int
     // of each stage.  Measured (16-bit, M = 2048): attn Wo 18.2 -> 14.3 us,
     // mlp Wo 22.9 -> 18.1 us; at M = 3072 the 2304-column shapes are faster
     // with 128 x 128 tiles (27.0 against 32.8 us).  Every output keeps its
-    // MFMA sequence and epilogue, so the bits do not change.
-    if constexpr (QB == 0) {
-      const int64_t t128 = ((M + 127) / 128) * ((N + (GEGLU ? 63 : 127)) / (GEGLU ? 64 : 128));
-      if (t128 <= cus + cus / 8) {
-        launch_mfma<128, 64, 4, 1, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
-        return;
-      }
+    // MFMA sequence and epilogue, so the bits do not change.  Quantized
+    // weights take the same rule (their loader dequantizes each stage of
+    // the thinner W tile; hb_qlinear calls with a quantized weight wherever
+    // these tiles are taken below M = 4096).
+    if (thin_tiles(M, N, GEGLU, cus)) {
+      launch_mfma<128, 64, 4, 1, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
+      return;
     }
     launch_mfma<128, 128, 2, 2, BF16, GEGLU, QB, AFF, SF32>(st, x, ldx, w, qw, bias, r, ldr, y, ldy, M, N, K);
   }
