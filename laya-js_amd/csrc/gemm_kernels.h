@@ -982,7 +982,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // ---- spread write-out.  With several tiles per block, an interior tile
   // leaves the C tile during the next tile's first six stages instead of in
   // one burst: stage s stores chunks WO_PS * s .. WO_PS * s + WO_PS - 1 of
-  // each thread's WO_N, as buffer stores issued after the stage's loads.
+  // each thread's WO_N (those below WO_N), as buffer stores issued after the
+  // stage's loads.
   // The wait counter counts loads and stores in issue order, so after a
   // burst the next tile's first load wait also waits for every store of the
   // tile, which all CUs issue at once; spread, a stage's stores are younger
@@ -996,8 +997,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // t / WTPR + WRPP * (q / WCPT)); panel-order Y chunk t + NT q as in
   // panel_chunk, whose row block and block column are wave-uniform (lane
   // offset 16 * lane, scalar block offset).
-  constexpr int WO_N = BM * CPR / NT, WO_PS = WO_N / 6;
-  static_assert(QKV || WO_N % 6 == 0, "spread write-out: whole chunks per stage");
+  constexpr int WO_N = BM * CPR / NT, WO_PS = (WO_N + 5) / 6;
   constexpr int WTPR = CPR % 8 == 0 ? 8 : 4, WCPT = CPR / WTPR, WRPP = NT / WTPR;
   // The layout is a compile-time one, panel order for GeGLU (whose output
   // feeds the next linear) and row-major otherwise; an output in the other
@@ -1021,6 +1021,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int ln = t0 & 63, r32 = ln & 31, lx = (ln >> 5) ^ (r32 & 7);
 #pragma unroll
       for (int u = 0; u < WO_PS; u++) {
+        if (S * WO_PS + u >= WO_N) break;
         const int rest = wv + (NT / 64) * (S * WO_PS + u);
         const int rb = rest / (CPR / 2), nb = rest - rb * (CPR / 2);
         const int slot = (nb >> 2) * (BM * 8) + (rb * 32 + r32) * 8 + (((nb & 3) * 2) ^ lx);
@@ -1033,6 +1034,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int voff = (wtr * ld2) + wtc * 16;
 #pragma unroll
       for (int u = 0; u < WO_PS; u++) {
+        if (S * WO_PS + u >= WO_N) break;
         const int q = S * WO_PS + u, pass = q / WCPT, j = q % WCPT;
         const int cr = wtc + WTPR * j;
         const int slot = (cr >> 3) * (BM * 8) + (wtr + WRPP * pass) * 8 + ((cr & 7) ^ (wtr & 7));
@@ -1184,14 +1186,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // substep; the write-out's C-tile reads ride with the last loads, its
     // stores follow every load; the W staging for the next stage goes last
     constexpr int NVMEM = TM * KS + B_LD, NPAIR = KS * TN, WOS = WO ? WO_PS : 0;
-    static_assert(NVMEM + 2 + WOS <= NPAIR, "write-out stores after the loads");
+    // the stores two pairs after the last load, or as late as they fit
+    constexpr int WST = NVMEM + 2 + WOS <= NPAIR ? NVMEM + 2 : NPAIR - WOS;
+    static_assert(NVMEM <= NPAIR && WST > NVMEM - WOS && WST + WOS <= NPAIR, "write-out stores after their reads");
     __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);
 #pragma unroll
     for (int p = 0; p < NPAIR; p++) {
       if (p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       if (p < (KS - 1) * TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       if (p >= NVMEM - WOS && p < NVMEM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (p >= NVMEM + 2 && p < NVMEM + 2 + WOS) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
+      if (p >= WST && p < WST + WOS) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);
     }
     store_b((g + 1) & 1, bs);
@@ -1488,6 +1492,17 @@ void mfma_dispatch(hipStream_t st, int cus, unsigned pan, const uint16_t* x, int
   // tiles.  K % 64 != 0 takes the large-M variant with a K tail.
   if constexpr (QB == 0) {
     if (arow_path(M)) {
+      // 128-column tiles where N is a multiple of 128 and not of 192 (N =
+      // 1024: 8 whole tiles instead of 5 1/3 of 192 columns)
+      if constexpr (!GEGLU) {
+        if (N % 192 != 0 && N % 128 == 0) {
+          if (K % 64 == 0)
+            launch_arow<128, BF16, false, false>(st, cus, pan, x, ldx, w, bias, r, ldr, y, ldy, M, N, K);
+          else
+            launch_arow<128, BF16, false, true>(st, cus, pan, x, ldx, w, bias, r, ldr, y, ldy, M, N, K);
+          return;
+        }
+      }
       if (K % 64 == 0)
         launch_arow<192, BF16, GEGLU, false>(st, cus, pan, x, ldx, w, bias, r, ldr, y, ldy, M, N, K);
       else
