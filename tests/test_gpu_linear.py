@@ -168,11 +168,10 @@ def test_qlinear_config2(b, name, M, bits):
 def test_qlinear_bf16(b, M, bits):
     """Quantized weights with bf16 activations: the dequantized weight is
     rounded once to bf16 (quant.ts:189-243, dequantRows then the compute
-    dtype) on every path -- M = 512 (the 128 x 128 kernel dequantizing in its
-    loader), M = 2048 (the weight dequantized once, then the 128 x 128
-    kernel) and M = 4160 (dequantized once, then the large-M kernel with a
-    partial row tile) -- against the oracle's dequantize-then-linear in bf16,
-    max-rel <= 1e-2."""
+    dtype) on every path -- M = 512 and M = 2048 (128 x 64 tiles, the loader
+    dequantizing each stage) and M = 4160 (dequantized once, then the
+    large-M kernel with a partial row tile) -- against the oracle's
+    dequantize-then-linear in bf16, max-rel <= 1e-2."""
     from laya_hip import compose as C
     N, K = SHAPES["Wqkv"]
     rng = np.random.default_rng(7 * M + bits)
@@ -233,6 +232,48 @@ def test_quantized_small_m_slab_bits_equal_large_m(b, dtype):
         rb = np.concatenate([r, rounded(rng.standard_normal((4096 - M, N)), dtype)])
         big, _ = run(xb, rb)
         np.testing.assert_array_equal(out, big[:M])
+        C.dispose_quantized(b, Q)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_quantized_mid_m_bits_equal_large_m(b, dtype):
+    """Between M = 1024 and 4096 a quantized linear on 128 x 64 tiles
+    dequantizes each W stage in its loader (Wqkv at M = 2048, attn Wo and
+    mlp Wo); Wqkv at M = 3072 runs 128 x 128 tiles on the weight dequantized
+    once into a 16-bit copy.  Every path gives a row the same bits: the rows
+    of an M-row call equal the same rows inside a 4096-row call, which the
+    large-M kernel computes on the weight dequantized once.  Each call is
+    also checked against the oracle's dequantize-then-linear (max-rel <=
+    1e-2).  q8 symmetric and q4 affine, residuals, a ragged M."""
+    from laya_hip import compose as C
+    rng = np.random.default_rng(43)
+    cases = [(2048, 2304, 768, 8, False), (3072, 2304, 768, 4, False), (2048, 768, 768, 4, True),
+             (1024, 768, 1152, 8, False), (2000, 768, 768, 8, True)]
+    for (M, N, K, bits, resid) in cases:
+        print(f"quantized mid-M M={M} N={N} K={K} q{bits} resid={resid} {dtype}", flush=True)
+        h, q, sf, zf = _quantized(rng, N, K, bits)
+        Q = C.upload_quantized(b, h, dtype)
+        assert Q.native
+        x = rounded(rng.standard_normal((4096, K)), dtype)
+        r = rounded(rng.standard_normal((4096, N)), dtype)
+
+        def run(xs, rs):
+            X, R = b.fromHost(to_host(xs, dtype)), b.fromHost(to_host(rs, dtype))
+            y = C.quantized_linear(b, X, Q)
+            y = b.add(R, y) if resid else y
+            out = np.asarray(b.read(y).data)
+            got = read32(b, y)
+            for t in (X, R, y):
+                b.dispose(t)
+            return out, got
+
+        (small, got), (big, _) = run(x[:M], r[:M]), run(x, r)
+        np.testing.assert_array_equal(small, big[:M])
+        rows = _rows(M, rng)
+        lin = cr.quantized_linear(x[rows], q, sf, zf, 64, dtype=dtype)
+        ref = r[rows] + rounded(lin, dtype) if resid else lin
+        err = max_rel(got[rows], ref)
+        assert err <= 1e-2, f"M={M} N={N} K={K} q{bits}: max-rel {err:.2e}"
         C.dispose_quantized(b, Q)
 
 
