@@ -68,6 +68,9 @@ CASES = [
     (16384, 2304, 832, True, False, False),    # GeGLU, 13 stages (a tail of 1)
     (16384, 2304, 896, False, True, False),    # 14 stages (a tail of 2)
     (8192, 2304, 960, False, False, True),     # 15 stages (a tail of 3), residual
+    (16384, 2304, 1000, False, True, False),   # K % 64 != 0 (a zeroed K tail) over 16 stages, streamed
+    (32768, 1024, 1000, False, False, True),   # 128-column tiles with a K tail and a residual
+    (16384, 2304, 1000, True, False, False),   # GeGLU with a K tail, streamed
 ]
 
 
