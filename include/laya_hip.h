@@ -215,9 +215,10 @@ int hb_linear_qkv(uintptr_t ctx, int dt, uintptr_t x, int64_t ldx, uintptr_t w, 
  * `zeros` are f16 [N, ceil(K/group)].  Weights dequantize to
  * fl16(q*s + z) (fl16(q*s) when symmetric), exactly what host
  * dequantization uploads, and feed the f16 MFMA with f32 accumulation
- * (M >= 4096, or M >= 1024 outside the small-M slab kernel: once per call
- * into a 16-bit copy taken from the context's pool for the duration of the
- * call; otherwise inside the GEMM kernels).
+ * (M >= 4096, and M >= 1024 for calls that neither the small-M slab
+ * kernel nor 128 x 64 tiles take: once per call into a 16-bit copy taken
+ * from the context's pool for the duration of the call; otherwise inside
+ * the GEMM kernels' weight loaders).
  * Backend.quantizedLinear (index.ts:257-261) via compose.quantizedLinear
  * (compose.ts:407-414).
  *  dt     dtype of x / y / resid / bias: HB_F16, HB_BF16 or HB_F32.
